@@ -1,0 +1,282 @@
+"""Benchmark: the Llama-3.2-1B decode-step GEMM set on one MI355X.
+
+A "step" is one decode step's worth of linear layers for a batch of M rows
+(BASELINE config 2 + config 3): for each of 16 layers, fused QKV (N=3072, K=2048,
+RoPE + bf16 KV append), O + residual (2048 x 2048), gate+up + SiLU (2 x 8192 x
+2048) and down + residual (2048 x 8192), then the LM head with greedy argmax
+(128256 x 2048). Weights are random-init bf16 ~N(0, 0.02) in the reference tile
+layout, 16 distinct layers (2.47 GB per step, far above the 256 MB MALL), so the
+weights stream from HBM as in a real decode. Inputs are resident in HBM before
+the timed region. Attention, norms and embedding are not GEMMs and are not in the
+step; their activation buffers hold fixed synthetic tiles.
+
+value = decode tokens/s of the GEMM path = M * steps / time.
+
+Printed as one JSON line with a per-GEMM table (GB/s, TFLOP/s, fraction of the
+HBM roofline at decode, of the MFMA roofline at prefill), the roofline object of
+the dominant kernel measured live with HIP events on the launch stream, and a CPU
+baseline: the reference's exact path (oracle/_ref) timed on this host's cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+LAYERS, HIDDEN, FFN, HEADS, KV_HEADS, HEAD_DIM, VOCAB = 16, 2048, 8192, 32, 8, 64, 128256
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--m", type=int, default=128, help="decode batch (activation rows)")
+    ap.add_argument("--table", type=int, default=1, help="per-GEMM table over M (0 to skip)")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline budget (0 to skip)")
+    ap.add_argument("--cpu-threads", type=int, default=16)
+    return ap.parse_args()
+
+
+class Model:
+    """Random-init Llama-3.2-1B-shaped weights in tile layout, on the GPU."""
+
+    def __init__(self, torch, dev):
+        from stride_amd import layout
+
+        g = torch.Generator(device=dev).manual_seed(0)
+
+        def w(n, k, rows=None):
+            t = (torch.randn(n, k, generator=g, device=dev) * 0.02).to(torch.bfloat16).view(torch.int16)
+            return layout.pack_tiles(t, rows)
+
+        self.layers = []
+        for _ in range(LAYERS):
+            self.layers.append(dict(
+                q=w(HEADS * HEAD_DIM, HIDDEN, layout.rope_rows(HEADS * HEAD_DIM, HEAD_DIM)),
+                k=w(KV_HEADS * HEAD_DIM, HIDDEN, layout.rope_rows(KV_HEADS * HEAD_DIM, HEAD_DIM)),
+                v=w(KV_HEADS * HEAD_DIM, HIDDEN, layout.rope_rows(KV_HEADS * HEAD_DIM, HEAD_DIM)),
+                o=w(HIDDEN, HEADS * HEAD_DIM), w1=w(FFN, HIDDEN), w3=w(FFN, HIDDEN), w2=w(HIDDEN, FFN)))
+        self.lm = w(VOCAB, HIDDEN)
+        torch.cuda.synchronize()
+
+
+class Buffers:
+    def __init__(self, torch, dev, m):
+        from stride_amd import harness, layout
+        from stride_amd.harness import PagedKv
+
+        g = torch.Generator(device=dev).manual_seed(1)
+        T = (m + 15) // 16
+        self.m = m
+
+        def act(k):
+            x = (torch.randn(m, k, generator=g, device=dev)).to(torch.bfloat16).view(torch.int16)
+            return layout.lane_tiles(x, T)
+
+        self.x = act(HIDDEN)
+        self.attn = act(HEADS * HEAD_DIM)
+        self.h = layout.lane_tiles(torch.randn(m, HIDDEN, generator=g, device=dev), T)
+        self.z = torch.zeros((T, FFN // 16, 16, 16), dtype=torch.int16, device=dev)
+        self.q = torch.zeros((m, HEADS * HEAD_DIM), dtype=torch.float32, device=dev)
+        self.kv = PagedKv.create(m, 16, KV_HEADS, HEAD_DIM, LAYERS, 16, dev, shuffle_seed=3)
+        half = HEAD_DIM // 2
+        pos = torch.arange(17, dtype=torch.float64, device=dev)[:, None]
+        inv = 1.0 / (500000.0 ** (torch.arange(half, dtype=torch.float64, device=dev) * 2 / HEAD_DIM))
+        ang = pos * inv
+        self.rope = torch.stack([ang.cos(), ang.sin()], dim=-1).float().contiguous()
+        self.slots = torch.arange(m, dtype=torch.int32, device=dev)
+        self.pos = torch.full((m,), 10, dtype=torch.int32, device=dev)
+        self.best = harness.best_init(m, dev)
+
+
+def step_ops(model, b):
+    """The launches of one decode step, as (name, callable) pairs."""
+    from stride_amd import harness
+
+    ops = []
+    m = b.m
+    for li, L in enumerate(model.layers):
+        ops.append(("qkv", lambda L=L, li=li: harness.qkv(L["q"], L["k"], L["v"], b.x, m, HEAD_DIM, b.rope, b.slots,
+                                                          b.pos, b.kv, layer=li, q_out=b.q)))
+        ops.append(("o", lambda L=L: harness.gemm_residual(L["o"], b.attn, b.h, m)))
+        ops.append(("gate_up", lambda L=L: harness.mlp13(L["w1"], L["w3"], b.x, m, out=b.z)))
+        ops.append(("down", lambda L=L: harness.gemm_residual(L["w2"], b.z, b.h, m)))
+    ops.append(("lm_head", lambda: harness.lm_greedy(model.lm, b.x, m, VOCAB, best=b.best)))
+    return ops
+
+
+# Algorithmic work per launch: FLOPs = 2 M N K; bytes = weights + activations in +
+# outputs (fp32 h read+write for residual GEMMs; bf16 z; fp32 q + bf16 k, v; 8 B
+# per row for the argmax).
+def work(name, m):
+    if name == "qkv":
+        n, k = (HEADS + 2 * KV_HEADS) * HEAD_DIM, HIDDEN
+        out = 4 * m * HEADS * HEAD_DIM + 2 * m * 2 * KV_HEADS * HEAD_DIM
+    elif name == "o":
+        n, k = HIDDEN, HEADS * HEAD_DIM
+        out = 8 * m * n
+    elif name == "gate_up":
+        n, k = 2 * FFN, HIDDEN
+        out = 2 * m * FFN
+    elif name == "down":
+        n, k = HIDDEN, FFN
+        out = 8 * m * n
+    else:
+        n, k = VOCAB, HIDDEN
+        out = 8 * m
+    return 2.0 * m * n * k, 2.0 * n * k + 2.0 * m * k + out
+
+
+def time_ops(torch, ops, reps):
+    """Average device time per launch of each op name, from HIP events recorded on
+    the stream the kernels are launched on (torch's current stream)."""
+    stream = torch.cuda.current_stream()
+    names = sorted({n for n, _ in ops})
+    res = {}
+    for name in names:
+        sel = [f for n, f in ops if n == name]
+        for f in sel:
+            f()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            for f in sel:
+                f()
+        e1.record(stream)
+        e1.synchronize()
+        res[name] = e0.elapsed_time(e1) / 1e3 / (reps * len(sel))
+    return res
+
+
+def cpu_baseline(seconds, threads):
+    """The reference's exact path (oracle/_ref: its src/kernels.cu compiled as C++)
+    on this host: one decode step at batch 1, sampled as one layer's four GEMMs
+    plus the LM head and scaled to 16 layers."""
+    import ctypes as C
+
+    import numpy as np
+
+    os.environ.setdefault("STRIDE_CPU_THREADS", str(threads))
+    from oracle import oracle as orc
+
+    kind = "reference" if orc.ref_available() else "port"
+    rng = np.random.default_rng(0)
+
+    def wts(n, k):
+        return (rng.standard_normal((n, k), dtype=np.float32) * 0.02).view(np.uint32).__rshift__(16).astype(np.uint16)
+
+    x1 = rng.standard_normal((1, HIDDEN), dtype=np.float32)
+    x2 = rng.standard_normal((1, FFN), dtype=np.float32)
+    shapes = [("qkv", 3072, HIDDEN, x1), ("o", HIDDEN, HIDDEN, x1), ("gate_up", 2 * FFN, HIDDEN, x1),
+              ("down", HIDDEN, FFN, x2), ("lm_head", VOCAB, HIDDEN, x1)]
+    t = {}
+    if kind == "reference":
+        lib = C.CDLL(orc.REF_PATH)
+        lib.ref_bench_gemm.restype = C.c_double
+        lib.ref_bench_gemm.argtypes = [np.ctypeslib.ndpointer(np.uint16, flags="C_CONTIGUOUS"), C.c_int, C.c_int,
+                                       np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS"), C.c_int, C.c_int]
+        budget = seconds / len(shapes)
+        for name, n, k, x in shapes:
+            w = wts(n, k)
+            one = lib.ref_bench_gemm(w, n, k, x, 1, 1)
+            reps = max(1, min(50, int(budget / max(one, 1e-6))))
+            t[name] = lib.ref_bench_gemm(w, n, k, x, 1, reps) / reps
+            del w
+    else:
+        ex = orc.Exact(threads=threads)
+        for name, n, k, x in shapes:
+            w = wts(n, k)
+            t0 = time.perf_counter()
+            ex.gemm(w, x)
+            t[name] = time.perf_counter() - t0
+    step = LAYERS * (t["qkv"] + t["o"] + t["gate_up"] + t["down"]) + t["lm_head"]
+    return {"value": round(1.0 / step, 3), "unit": "tok/s", "cores": threads, "kind": kind,
+            "sample": "batch-1 decode step, exact path: one layer's QKV/O/gate+up/down GEMMs + LM head timed "
+                      "(k_lm_full order, all fmaf chains), layer time x16 + LM head; STRIDE_CPU_THREADS="
+                      f"{threads}", "seconds_per_step": round(step, 4),
+            "per_gemm_ms": {k: round(v * 1e3, 3) for k, v in t.items()}}
+
+
+def main():
+    a = parse()
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build runs on one GPU only (the GEMM path has no multi-GPU part); "
+              "use --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from stride_amd import _lib
+
+    _lib.load()  # fail loudly without the HIP library
+    dev = "cuda:0"
+    torch.cuda.set_device(0)
+    model = Model(torch, dev)
+    b = Buffers(torch, dev, a.m)
+    ops = step_ops(model, b)
+
+    for _ in range(a.warmup):
+        for _, f in ops:
+            f()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(a.steps):
+        for _, f in ops:
+            f()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    ms_step = dt / a.steps * 1e3
+    value = a.m * a.steps / dt
+
+    # Per-kernel averages at the bench M (dominant kernel -> roofline object).
+    per = time_ops(torch, ops, 3)
+    share = {n: per[n] * sum(1 for o, _ in ops if o == n) for n in per}
+    dom = max(share, key=share.get)
+    fl, by = work(dom, a.m)
+    ach = by / per[dom] / 1e9
+    roof = {"kernel": dom, "bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None, "avg_launch_us": round(per[dom] * 1e6, 2),
+            "algorithmic_bytes": int(by)}
+    weight_bytes = sum(work(n, 0)[1] for n, _ in ops)
+
+    table = []
+    if a.table:
+        for m in (1, 8, 32, 64, 128, 290, 1024, 2048, 4096):
+            bm = b if m == a.m else Buffers(torch, dev, m)
+            t = time_ops(torch, step_ops(model, bm), 2 if m >= 1024 else 3)
+            row = {"M": m}
+            for n, sec in sorted(t.items()):
+                f, byt = work(n, m)
+                gbs, tfl = byt / sec / 1e9, f / sec / 1e12
+                bound = "hbm" if m <= 128 else "mfma"
+                frac = gbs / HBM_PEAK_GBS if bound == "hbm" else tfl / MFMA_BF16_PEAK_TFLOPS
+                row[n] = {"us": round(sec * 1e6, 2), "GB/s": round(gbs, 1), "TFLOP/s": round(tfl, 2),
+                          "frac": round(frac, 4), "bound": bound}
+            table.append(row)
+            del bm
+            torch.cuda.empty_cache()
+
+    cpu = cpu_baseline(a.cpu_seconds, a.cpu_threads) if a.cpu_seconds > 0 else None
+    out = {
+        "metric": "Llama-3.2-1B GEMM GB/s & TFLOP/s (% roofline) at M=1..4096; decode tok/s",
+        "value": round(value, 1), "unit": "tok/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic (random-init bf16 weights ~N(0,0.02), activations ~N(0,1))",
+        "config": {"workload": f"decode-step GEMM set, Llama-3.2-1B shapes, 16 layers + LM head greedy, M={a.m}",
+                   "M": a.m, "layers": LAYERS, "weight_bytes_per_step": int(weight_bytes),
+                   "step_GB/s": round(weight_bytes / (ms_step / 1e3) / 1e9, 1), "parallelism": "single-gpu"},
+        "roofline": roof, "cpu_baseline": cpu, "gemm_table": table,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,167 @@
+/* C ABI of the MI355X (gfx950) batch-invariant BF16 linear-layer GEMM library
+ * (libstride_tc.so). It replaces the GEMM entry points of stride's tensor-core
+ * path, declared in the reference at src/kernels_tc.h:81-87 and defined at
+ * src/kernels_tc.cu:677-710.
+ *
+ * Structs are byte-compatible with the reference's POD parameter blocks
+ * (src/kernels.h:112-135, 213-217 and src/kernels_tc.h:27-77): same field order,
+ * int32 fields, 8-byte pointers, BestEntry 8-byte aligned. A caller that already
+ * fills stride::TcGemmResidualParams can pass its address here unchanged.
+ *
+ * Layouts (the reference's tile conventions, src/kernels_tc.cu:8-11):
+ *   weights  W[row tile][col tile][16 rows][16 cols]  bf16 (pack_tiles, src/model.cpp:114-133)
+ *   x / z    X[lane tile][col tile][16 lanes][16 cols] bf16
+ *   h        fp32, same tile grid as x: h[lane tile][row tile][16 lanes][16 rows]
+ *   logits   fp32 [row tile][lane tile][16 rows][16 lanes]
+ * Shapes: cols (K) must be a multiple of 32; lane_groups must equal ceil(rows/16);
+ * lanes past `rows` inside the last lane tile must hold zeros (the engine
+ * zero-fills its tile buffers, src/engine.cpp:72-80).
+ *
+ * Batch invariance: every output element is computed by the same sequence of
+ * operations whatever `rows`, the lane position, the stream or the (r, lt)
+ * blocking hint: K is consumed in 32-column chunks in ascending order by one
+ * v_mfma_f32_16x16x32_bf16 chain per split, the split count S depends only on
+ * the weight shape (stride_tc_split_count), and the S partial sums combine left
+ * to right, split 0 starting from the residual where there is one.
+ *
+ * Errors: every entry point returns 0 on success or a nonzero code (a hipError_t
+ * value, or STRIDE_TC_EINVAL for rejected arguments); stride_tc_last_error()
+ * describes the last failure on the calling thread. Launches are asynchronous on
+ * `stream` (NULL = the default stream); nothing here synchronizes or allocates.
+ */
+#ifndef STRIDE_TC_H
+#define STRIDE_TC_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define STRIDE_TC_EINVAL 0x5354 /* argument rejected before any launch */
+
+/* src/kernels.h:112-116 */
+typedef struct StrideGemmMat {
+  const uint16_t* w;
+  int32_t groups; /* row tiles (N / 16) */
+  int32_t cols;   /* K */
+} StrideGemmMat;
+
+/* src/kernels.h:119-128. The page size in tokens is group_elems / head_dim
+ * (64 in the reference's KvCache; any power of two here). */
+typedef struct StrideKvRef {
+  void* arena;
+  const int32_t* table;
+  int64_t block_elems;
+  int64_t layer_elems;
+  int64_t which_elems;
+  int64_t group_elems;
+  int32_t max_blocks;
+  int32_t head_dim;
+} StrideKvRef;
+
+/* src/kernels.h:130-135 (stride and bug are ignored by this library) */
+typedef struct StrideLanes {
+  int32_t rows;
+  int32_t lane_groups;
+  int32_t stride;
+  int32_t bug;
+} StrideLanes;
+
+/* src/kernels.h:214-217 */
+typedef struct StrideBestEntry {
+  float value;
+  int32_t index;
+} __attribute__((aligned(8))) StrideBestEntry;
+
+/* src/kernels_tc.h:27-39 */
+typedef struct StrideTcQkvParams {
+  StrideLanes l;
+  const uint16_t* x;
+  StrideGemmMat q, k, v;
+  float* q_out;
+  int32_t q_stride;
+  StrideKvRef kv;
+  const float* rope;
+  const int32_t* row_slot;
+  const int32_t* row_pos;
+  int32_t layer;
+  int32_t head_dim;
+} StrideTcQkvParams;
+
+/* src/kernels_tc.h:41-46 */
+typedef struct StrideTcGemmResidualParams {
+  StrideLanes l;
+  const uint16_t* x;
+  StrideGemmMat m;
+  float* h;
+} StrideTcGemmResidualParams;
+
+/* src/kernels_tc.h:48-53 */
+typedef struct StrideTcMlp13Params {
+  StrideLanes l;
+  const uint16_t* x;
+  StrideGemmMat w1, w3;
+  uint16_t* z;
+} StrideTcMlp13Params;
+
+/* src/kernels_tc.h:64-70 */
+typedef struct StrideTcLmGreedyParams {
+  StrideLanes l;
+  const uint16_t* x;
+  StrideGemmMat m;
+  int32_t vocab;
+  StrideBestEntry* best;
+} StrideTcLmGreedyParams;
+
+/* src/kernels_tc.h:72-77 */
+typedef struct StrideTcLmFullParams {
+  StrideLanes l;
+  const uint16_t* x;
+  StrideGemmMat m;
+  float* logits;
+} StrideTcLmFullParams;
+
+/* Replaces stride::tc_qkv (src/kernels_tc.h:81, src/kernels_tc.cu:677-679):
+ * q = Wq x, k = Wk x, v = Wv x with RoPE on q and k (row tiles hold RoPE pairs
+ * (d0+i, d0+D/2+i), src/model.cpp:178-183); q -> fp32 q_out[row*q_stride +
+ * head*D + d]; k, v -> bf16 (round to nearest even) into the paged KV arena. */
+int stride_tc_qkv(const StrideTcQkvParams* p, void* stream);
+
+/* Replaces stride::tc_gemm_residual (src/kernels_tc.h:83, src/kernels_tc.cu:692-695):
+ * h <- h + W x (output and MLP-down projections). row_tiles_per_warp and
+ * lane_tiles_per_warp are the reference's register-blocking hints; they are
+ * accepted for interface compatibility and never change results. */
+int stride_tc_gemm_residual(const StrideTcGemmResidualParams* p, int row_tiles_per_warp, int lane_tiles_per_warp,
+                            void* stream);
+
+/* Replaces stride::tc_mlp13 (src/kernels_tc.h:84, src/kernels_tc.cu:696-700):
+ * z = bf16(det_silu(W1 x) * (W3 x)) written as x-layout tiles. */
+int stride_tc_mlp13(const StrideTcMlp13Params* p, int row_tiles_per_warp, int lane_tiles_per_warp, void* stream);
+
+/* Replaces stride::tc_lm_greedy (src/kernels_tc.h:86, src/kernels_tc.cu:702-706):
+ * per lane, best[lane] <- lexicographic max of (logit, -index) over rows < vocab,
+ * merged into the caller-initialised entries (value -inf, index -1). */
+int stride_tc_lm_greedy(const StrideTcLmGreedyParams* p, int row_tiles_per_warp, int lane_tiles_per_warp,
+                        void* stream);
+
+/* Replaces stride::tc_lm_full (src/kernels_tc.h:87, src/kernels_tc.cu:707-710):
+ * logits tiles [row tile][lane tile][16 rows][16 lanes], fp32. */
+int stride_tc_lm_full(const StrideTcLmFullParams* p, int lane_tiles_per_block, void* stream);
+
+/* No reference counterpart (a property the reference fixes in code,
+ * src/kernels_tc.cu:29-32): the number of K splits used for a weight matrix
+ * of n rows and k columns. Depends on (n, k) only. */
+int stride_tc_split_count(int32_t n, int32_t k);
+
+/* Message for the last nonzero return on this thread ("" if none). */
+const char* stride_tc_last_error(void);
+
+/* Library version string. */
+const char* stride_tc_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* STRIDE_TC_H */

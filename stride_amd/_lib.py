@@ -1,0 +1,152 @@
+"""ctypes binding of libstride_tc.so (the C ABI declared in include/stride_tc.h).
+
+The Structure classes mirror the reference's POD parameter blocks byte for byte
+(src/kernels.h:112-135, 213-217; src/kernels_tc.h:27-77); ``check_layout`` asserts
+the sizes the C++ side static_asserts. Loading fails loudly: there is no fallback
+path, so a missing or stale library is an error, never a silent CPU substitute.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libstride_tc.so")
+
+EINVAL = 0x5354
+
+
+class GemmMat(C.Structure):  # src/kernels.h:112-116
+    _fields_ = [("w", C.c_void_p), ("groups", C.c_int32), ("cols", C.c_int32)]
+
+
+class KvRef(C.Structure):  # src/kernels.h:119-128
+    _fields_ = [
+        ("arena", C.c_void_p),
+        ("table", C.c_void_p),
+        ("block_elems", C.c_int64),
+        ("layer_elems", C.c_int64),
+        ("which_elems", C.c_int64),
+        ("group_elems", C.c_int64),
+        ("max_blocks", C.c_int32),
+        ("head_dim", C.c_int32),
+    ]
+
+
+class Lanes(C.Structure):  # src/kernels.h:130-135
+    _fields_ = [("rows", C.c_int32), ("lane_groups", C.c_int32), ("stride", C.c_int32), ("bug", C.c_int32)]
+
+
+class BestEntry(C.Structure):  # src/kernels.h:214-217
+    _fields_ = [("value", C.c_float), ("index", C.c_int32)]
+
+
+class TcQkvParams(C.Structure):  # src/kernels_tc.h:27-39
+    _fields_ = [
+        ("l", Lanes),
+        ("x", C.c_void_p),
+        ("q", GemmMat),
+        ("k", GemmMat),
+        ("v", GemmMat),
+        ("q_out", C.c_void_p),
+        ("q_stride", C.c_int32),
+        ("kv", KvRef),
+        ("rope", C.c_void_p),
+        ("row_slot", C.c_void_p),
+        ("row_pos", C.c_void_p),
+        ("layer", C.c_int32),
+        ("head_dim", C.c_int32),
+    ]
+
+
+class TcGemmResidualParams(C.Structure):  # src/kernels_tc.h:41-46
+    _fields_ = [("l", Lanes), ("x", C.c_void_p), ("m", GemmMat), ("h", C.c_void_p)]
+
+
+class TcMlp13Params(C.Structure):  # src/kernels_tc.h:48-53
+    _fields_ = [("l", Lanes), ("x", C.c_void_p), ("w1", GemmMat), ("w3", GemmMat), ("z", C.c_void_p)]
+
+
+class TcLmGreedyParams(C.Structure):  # src/kernels_tc.h:64-70
+    _fields_ = [("l", Lanes), ("x", C.c_void_p), ("m", GemmMat), ("vocab", C.c_int32), ("best", C.c_void_p)]
+
+
+class TcLmFullParams(C.Structure):  # src/kernels_tc.h:72-77
+    _fields_ = [("l", Lanes), ("x", C.c_void_p), ("m", GemmMat), ("logits", C.c_void_p)]
+
+
+# Symbols the library must export (everything include/stride_tc.h declares).
+EXPORTS = (
+    "stride_tc_qkv",
+    "stride_tc_gemm_residual",
+    "stride_tc_mlp13",
+    "stride_tc_lm_greedy",
+    "stride_tc_lm_full",
+    "stride_tc_split_count",
+    "stride_tc_last_error",
+    "stride_tc_version",
+)
+
+
+def check_layout() -> None:
+    """Sizes and offsets the C++ side static_asserts (reference PODs on x86-64)."""
+    assert C.sizeof(GemmMat) == 16
+    assert C.sizeof(KvRef) == 56
+    assert C.sizeof(Lanes) == 16
+    assert C.sizeof(BestEntry) == 8
+    assert TcQkvParams.kv.offset == 88 and C.sizeof(TcQkvParams) == 176
+    assert C.sizeof(TcGemmResidualParams) == 48
+    assert C.sizeof(TcMlp13Params) == 64
+    assert C.sizeof(TcLmGreedyParams) == 56
+    assert C.sizeof(TcLmFullParams) == 48
+
+
+class StrideTcError(RuntimeError):
+    """Raised when an entry point returns nonzero (the reference's device.cu
+    check() throws std::runtime_error for the same condition)."""
+
+
+_lib = None
+
+
+def load(path: str = LIB_PATH) -> C.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise ImportError(
+            f"libstride_tc.so not found at {path}; build it with "
+            "`python -c 'import __graft_entry__ as g; g.build()'` (there is no fallback path)")
+    lib = C.CDLL(path)
+    for name in EXPORTS:
+        getattr(lib, name)  # raises AttributeError if a symbol is missing
+    vp = C.c_void_p
+    lib.stride_tc_qkv.argtypes = [C.POINTER(TcQkvParams), vp]
+    lib.stride_tc_gemm_residual.argtypes = [C.POINTER(TcGemmResidualParams), C.c_int, C.c_int, vp]
+    lib.stride_tc_mlp13.argtypes = [C.POINTER(TcMlp13Params), C.c_int, C.c_int, vp]
+    lib.stride_tc_lm_greedy.argtypes = [C.POINTER(TcLmGreedyParams), C.c_int, C.c_int, vp]
+    lib.stride_tc_lm_full.argtypes = [C.POINTER(TcLmFullParams), C.c_int, vp]
+    for name in ("stride_tc_qkv", "stride_tc_gemm_residual", "stride_tc_mlp13", "stride_tc_lm_greedy",
+                 "stride_tc_lm_full", "stride_tc_split_count"):
+        getattr(lib, name).restype = C.c_int
+    lib.stride_tc_split_count.argtypes = [C.c_int32, C.c_int32]
+    lib.stride_tc_last_error.restype = C.c_char_p
+    lib.stride_tc_last_error.argtypes = []
+    lib.stride_tc_version.restype = C.c_char_p
+    lib.stride_tc_version.argtypes = []
+    check_layout()
+    _lib = lib
+    return lib
+
+
+def check(rc: int) -> None:
+    if rc != 0:
+        msg = load().stride_tc_last_error().decode()
+        raise StrideTcError(f"stride_tc error {rc:#x}: {msg}")
+
+
+def split_count(n: int, k: int) -> int:
+    s = load().stride_tc_split_count(n, k)
+    if s < 0:
+        check(s)
+    return s

@@ -1,0 +1,110 @@
+// Device-side building blocks shared by every GEMM kernel of libstride_tc:
+// MFMA fragment addressing on the reference tile layout, the deterministic
+// epilogue numerics, and the order-independent argmax update.
+//
+// Fragment geometry (v_mfma_f32_16x16x32_bf16, one wavefront of 64 lanes):
+//   A (weights, 16 rows x 32 k):  lane l holds row l%16, k = 8*(l/16) .. +7
+//   B (x, 32 k x 16 lanes):       lane l holds lane l%16, k = 8*(l/16) .. +7
+//   C/D (16 rows x 16 lanes fp32): lane l holds lane l%16, rows 4*(l/16) .. +3
+// A 32-column chunk of a row tile is two adjacent 16x16 tiles (1 KiB, contiguous
+// in the packed layout), and k-group g = l/16 of a lane lives in tile g/2, column
+// half g%2. So lane l reads 16 contiguous bytes at
+//   (g/2)*512 + (l%16)*32 + (g%2)*16
+// and one wavefront load instruction covers the 1 KiB chunk exactly once.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/stride_tc.h"
+
+namespace stride_tc {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kTileElems = 256;     // one 16x16 tile
+constexpr int kChunkBytes = 1024;   // 32 columns of one row/lane tile (two tiles)
+constexpr int kChunkCols = 32;
+constexpr int kWave = 64;
+
+// Byte offset of lane `lane`'s 16-byte fragment slice inside a 1 KiB chunk.
+__device__ __forceinline__ int frag_offset(int lane) {
+  const int g = lane >> 4;
+  return ((g >> 1) << 9) + ((lane & 15) << 5) + ((g & 1) << 4);
+}
+
+// Inverse map: the lane whose fragment slice is the 16-byte piece j of a chunk.
+__device__ __forceinline__ int frag_lane_of_piece(int j) {
+  const int tile = j >> 5, row = (j & 31) >> 1, half = j & 1;
+  return (((tile << 1) | half) << 4) | row;
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+__device__ __forceinline__ u32x4 load16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+
+__device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float f32_of(uint32_t u) { return __uint_as_float(u); }
+__device__ __forceinline__ uint32_t u32_of(float f) { return __float_as_uint(f); }
+
+// fp32 -> bf16, round to nearest even on the bit pattern (no NaN special case),
+// as the reference's bf16_round_bits (src/kernel_common.h:29-32).
+__device__ __forceinline__ uint32_t bf16_rne(float f) {
+  const uint32_t u = u32_of(f);
+  return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
+// Deterministic exp (src/numerics.h:16-30): k = floor(x*log2e + 1/2), two-part
+// Cody-Waite ln2 reduction, degree-6 Cephes polynomial by FMA, exponent scale.
+// Only correctly rounded operations (fma, floor, add) so the bits are fixed.
+__device__ __forceinline__ float det_exp(float x) {
+  if (x < -87.0f) return 0.0f;
+  if (x > 88.0f) return f32_of(0x7F800000u);
+  const float kf = floorf(fmaf(x, 1.44269504088896341f, 0.5f));
+  float r = fmaf(-kf, 0.693359375f, x);
+  r = fmaf(-kf, -2.12194440e-4f, r);
+  float p = 1.9875691500e-4f;
+  p = fmaf(p, r, 1.3981999507e-3f);
+  p = fmaf(p, r, 8.3334519073e-3f);
+  p = fmaf(p, r, 4.1665795894e-2f);
+  p = fmaf(p, r, 1.6666665459e-1f);
+  p = fmaf(p, r, 5.0000001201e-1f);
+  const float y = fmaf(fmaf(p, r, 1.0f), r, 1.0f);
+  return f32_of(u32_of(y) + (static_cast<uint32_t>(static_cast<int32_t>(kf)) << 23));
+}
+
+// x * sigmoid(x) as x / (1 + exp(-x)); the division is IEEE (hipcc's default
+// correctly rounded fp32 divide).
+__device__ __forceinline__ float det_silu(float x) { return x / (1.0f + det_exp(-x)); }
+
+// Lexicographic order on (value, -index): larger value wins, ties go to the
+// smaller index (src/kernel_common.h:58-60).
+__device__ __forceinline__ bool better_than(float v, int32_t i, float cv, int32_t ci) {
+  return v > cv || (v == cv && i < ci);
+}
+
+// Merge (value, index) into a BestEntry with a 64-bit compare-and-swap. The
+// result is the lexicographic max whatever order the updates arrive in
+// (src/kernel_common.h:64-82).
+__device__ __forceinline__ void best_update(StrideBestEntry* slot, float value, int32_t index) {
+  unsigned long long* word = reinterpret_cast<unsigned long long*>(slot);
+  const unsigned long long want =
+      (static_cast<unsigned long long>(static_cast<uint32_t>(index)) << 32) | u32_of(value);
+  unsigned long long seen = __hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (;;) {
+    const float cv = f32_of(static_cast<uint32_t>(seen));
+    const int32_t ci = static_cast<int32_t>(seen >> 32);
+    if (!better_than(value, index, cv, ci)) return;
+    const unsigned long long prev = atomicCAS(word, seen, want);
+    if (prev == seen) return;
+    seen = prev;
+  }
+}
+
+}  // namespace stride_tc

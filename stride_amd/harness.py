@@ -1,0 +1,128 @@
+"""Convenience runners over the operator surface for torch device tensors.
+
+Each runner fills the reference-shaped parameter block for one call of the C ABI
+and launches it on the current stream; tensors must already be in the tile
+layouts of stride_amd.layout. Used by the tests, the benchmark and smoke().
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import tc
+from .tc import (GemmMat, KvRef, TcGemmResidualParams, TcLmFullParams, TcLmGreedyParams, TcMlp13Params,
+                 TcQkvParams, lanes, mat, ptr)
+
+U16 = torch.int16  # bf16 bit patterns travel as int16 tensors
+
+
+def gemm_residual(w_tiles, x_tiles, h_tiles, rows: int, r: int = 1, lt: int = 1) -> None:
+    p = TcGemmResidualParams(lanes(rows), ptr(x_tiles), mat(w_tiles), ptr(h_tiles))
+    tc.tc_gemm_residual(p, r, lt)
+
+
+def lm_full(w_tiles, x_tiles, rows: int, out=None):
+    T = (rows + 15) // 16
+    if out is None:
+        out = torch.empty((w_tiles.shape[0], T, 16, 16), dtype=torch.float32, device=x_tiles.device)
+    p = TcLmFullParams(lanes(rows), ptr(x_tiles), mat(w_tiles), ptr(out))
+    tc.tc_lm_full(p, 1)
+    return out
+
+
+def mlp13(w1_tiles, w3_tiles, x_tiles, rows: int, out=None, r: int = 1, lt: int = 1):
+    T = (rows + 15) // 16
+    if out is None:
+        out = torch.zeros((T, w1_tiles.shape[0], 16, 16), dtype=U16, device=x_tiles.device)
+    p = TcMlp13Params(lanes(rows), ptr(x_tiles), mat(w1_tiles), mat(w3_tiles), ptr(out))
+    tc.tc_mlp13(p, r, lt)
+    return out
+
+
+def best_init(rows: int, device) -> torch.Tensor:
+    """BestEntry[rows] = {-inf, -1} as the engine uploads it (src/engine.cpp:423-424),
+    stored as int32 pairs (value bits, index)."""
+    b = torch.empty((rows, 2), dtype=torch.int32, device=device)
+    b[:, 0] = -8388608  # 0xFF800000 = -inf
+    b[:, 1] = -1
+    return b
+
+
+def lm_greedy(w_tiles, x_tiles, rows: int, vocab: int, best=None, r: int = 1, lt: int = 1):
+    if best is None:
+        best = best_init(rows, x_tiles.device)
+    p = TcLmGreedyParams(lanes(rows), ptr(x_tiles), mat(w_tiles), vocab, ptr(best))
+    tc.tc_lm_greedy(p, r, lt)
+    return best
+
+
+def best_split(best: torch.Tensor):
+    """(values fp32, indices int32) from a BestEntry buffer."""
+    b = best.cpu()
+    return b[:, 0].contiguous().view(torch.float32), b[:, 1].contiguous()
+
+
+@dataclass
+class PagedKv:
+    """A paged KV arena in the reference layout [block][layer][K|V][group][token][dim]
+    (src/kernels.h:9, src/kv_cache.cpp:10-40), bf16 elements."""
+
+    arena: torch.Tensor
+    table: torch.Tensor
+    ref: KvRef
+    page_tokens: int
+    max_blocks: int
+
+    @staticmethod
+    def create(slots: int, max_ctx: int, kv_heads: int, head_dim: int, layers: int, page_tokens: int, device,
+               shuffle_seed: int = 0) -> "PagedKv":
+        max_blocks = (max_ctx + page_tokens - 1) // page_tokens
+        group = page_tokens * head_dim
+        which = group * kv_heads
+        layer = which * 2
+        block = layer * layers
+        nblocks = slots * max_blocks
+        order = torch.arange(nblocks, dtype=torch.int32)
+        if shuffle_seed:
+            g = torch.Generator().manual_seed(shuffle_seed)
+            order = order[torch.randperm(nblocks, generator=g)]
+        table = order.reshape(slots, max_blocks).contiguous().to(device)
+        arena = torch.zeros(nblocks * block, dtype=U16, device=device)
+        ref = KvRef(ptr(arena), ptr(table), block, layer, which, group, max_blocks, head_dim)
+        return PagedKv(arena, table, ref, page_tokens, max_blocks)
+
+    def gather(self, layer: int, which: int, slots, positions, kv_heads: int, head_dim: int) -> torch.Tensor:
+        """Dense [rows][kv_heads * head_dim] bf16 bits of the entries at (slot, pos)."""
+        r = self.ref
+        tab = self.table.cpu()
+        rows = []
+        for s, p in zip(list(slots), list(positions)):
+            blk = int(tab[int(s), int(p) // self.page_tokens])
+            tok = int(p) % self.page_tokens
+            base = blk * r.block_elems + layer * r.layer_elems + which * r.which_elems + tok * head_dim
+            idx = torch.tensor([base + h * r.group_elems + d for h in range(kv_heads) for d in range(head_dim)],
+                               device=self.arena.device)
+            rows.append(self.arena[idx])
+        return torch.stack(rows)
+
+
+def qkv(wq_tiles, wk_tiles, wv_tiles, x_tiles, rows: int, head_dim: int, rope, row_slot, row_pos, kv: PagedKv,
+        layer: int = 0, q_out=None):
+    nq = wq_tiles.shape[0] * 16
+    if q_out is None:
+        q_out = torch.zeros((max(rows, 1), nq), dtype=torch.float32, device=x_tiles.device)
+    p = TcQkvParams()
+    p.l = lanes(rows)
+    p.x = ptr(x_tiles)
+    p.q, p.k, p.v = mat(wq_tiles), mat(wk_tiles), mat(wv_tiles)
+    p.q_out = ptr(q_out)
+    p.q_stride = nq
+    p.kv = kv.ref
+    p.rope = ptr(rope)
+    p.row_slot = ptr(row_slot)
+    p.row_pos = ptr(row_pos)
+    p.layer = layer
+    p.head_dim = head_dim
+    tc.tc_qkv(p)
+    return q_out

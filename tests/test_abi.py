@@ -1,0 +1,95 @@
+"""C-ABI library checks that need no GPU: it loads, exports every symbol that
+include/stride_tc.h declares, its structs are byte-compatible with the reference's
+parameter blocks, the split rule, and argument rejection before any launch."""
+import ctypes as C
+import os
+import re
+import subprocess
+
+import pytest
+
+from stride_amd import _lib
+from stride_amd import tc
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "stride_tc.h")
+REF_SRC = "/root/reference/src"
+
+
+def test_exports_match_header():
+    lib = _lib.load()
+    declared = set(re.findall(r"\b(stride_tc_\w+)\s*\(", open(HEADER).read()))
+    assert declared == set(_lib.EXPORTS)
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert b"gfx950" in lib.stride_tc_version()
+
+
+def test_ctypes_layout():
+    _lib.check_layout()
+
+
+PROBE = r"""
+#include <cstddef>
+#include <cstdio>
+#include HDR
+int main() {
+  printf("%zu %zu %zu %zu %zu %zu %zu %zu %zu %zu\n", sizeof(GM), sizeof(KV), sizeof(LN), sizeof(BE),
+         sizeof(QKV), offsetof(QKV, kv), offsetof(QKV, head_dim), sizeof(RES), sizeof(MLP), sizeof(LMG));
+}
+"""
+
+
+def _probe(tmp_path, include, names, extra=()):
+    src = tmp_path / "probe.cpp"
+    defs = "".join(f"#define {k} {v}\n" for k, v in names.items())
+    src.write_text(defs + PROBE.replace("HDR", f'"{include}"'))
+    exe = tmp_path / "probe"
+    subprocess.run(["g++", "-std=c++17", *extra, str(src), "-o", str(exe)], check=True)
+    return subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split()
+
+
+def test_struct_layout_matches_reference(tmp_path):
+    ours = _probe(tmp_path, HEADER, dict(GM="StrideGemmMat", KV="StrideKvRef", LN="StrideLanes", BE="StrideBestEntry",
+                                         QKV="StrideTcQkvParams", RES="StrideTcGemmResidualParams",
+                                         MLP="StrideTcMlp13Params", LMG="StrideTcLmGreedyParams"))
+    assert ours == ["16", "56", "16", "8", "176", "88", "172", "48", "64", "56"]
+    if not os.path.exists(os.path.join(REF_SRC, "kernels_tc.h")):
+        pytest.skip("reference tree absent")
+    theirs = _probe(tmp_path, os.path.join(REF_SRC, "kernels_tc.h"),
+                    dict(GM="stride::GemmMat", KV="stride::KvRef", LN="stride::Lanes", BE="stride::BestEntry",
+                         QKV="stride::TcQkvParams", RES="stride::TcGemmResidualParams", MLP="stride::TcMlp13Params",
+                         LMG="stride::TcLmGreedyParams"))
+    assert ours == theirs
+
+
+def test_split_rule():
+    cases = {(2048, 2048): 8, (3072, 2048): 8, (512, 2048): 8, (2048, 8192): 8, (8192, 2048): 2,
+             (128256, 2048): 1, (16, 64): 2, (16, 32): 1, (64, 96): 3, (64, 160): 5, (64, 192): 6}
+    for (n, k), s in cases.items():
+        assert tc.split_count(n, k) == s, (n, k)
+    with pytest.raises(_lib.StrideTcError):
+        tc.split_count(16, 48)
+
+
+def test_rejects_bad_arguments_without_launch():
+    lib = _lib.load()
+    p = tc.TcGemmResidualParams(tc.Lanes(17, 1, 0, 0), 0x1000, tc.GemmMat(0x2000, 4, 64), 0x3000)
+    assert lib.stride_tc_gemm_residual(C.byref(p), 1, 1, None) == _lib.EINVAL
+    assert b"lane_groups" in lib.stride_tc_last_error()
+    p = tc.TcGemmResidualParams(tc.Lanes(17, 2, 0, 0), 0x1000, tc.GemmMat(0x2000, 4, 48), 0x3000)
+    assert lib.stride_tc_gemm_residual(C.byref(p), 1, 1, None) == _lib.EINVAL
+    assert b"multiple of 32" in lib.stride_tc_last_error()
+    g = tc.TcLmGreedyParams(tc.Lanes(1, 1, 0, 0), 0x1000, tc.GemmMat(0x2000, 4, 64), 65, 0x3000)
+    with pytest.raises(tc.StrideTcError, match="vocab"):
+        _lib.check(lib.stride_tc_lm_greedy(C.byref(g), 1, 1, None))
+    q = tc.TcQkvParams()
+    q.l = tc.Lanes(1, 1, 0, 0)
+    q.x = 0x1000
+    q.q = q.k = q.v = tc.GemmMat(0x2000, 4, 64)
+    q.head_dim = 24
+    assert lib.stride_tc_qkv(C.byref(q), None) == _lib.EINVAL
+    assert lib.stride_tc_mlp13(None, 1, 1, None) == _lib.EINVAL
+    # rows == 0 is a no-op, as the reference's launch<> with zero blocks
+    z = tc.TcGemmResidualParams(tc.Lanes(0, 0, 0, 0), 0x1000, tc.GemmMat(0x2000, 4, 64), 0x3000)
+    assert lib.stride_tc_gemm_residual(C.byref(z), 1, 1, None) == 0
