@@ -43,6 +43,8 @@ def parse():
     ap.add_argument("--table", type=int, default=1, help="per-GEMM table over M (0 to skip)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline budget (0 to skip)")
     ap.add_argument("--cpu-threads", type=int, default=16)
+    ap.add_argument("--copy-calib-mib", type=int, default=0,
+                    help="also run one plain device copy of this size (calibrates FETCH_SIZE/WRITE_SIZE counters)")
     return ap.parse_args()
 
 
@@ -222,6 +224,13 @@ def main():
     model = Model(torch, dev)
     b = Buffers(torch, dev, a.m)
     ops = step_ops(model, b)
+
+    if a.copy_calib_mib:
+        src = torch.ones(a.copy_calib_mib << 18, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        torch.neg(src, out=dst)  # a plain streaming kernel: reads and writes exactly N bytes
+        torch.cuda.synchronize()
+        del src, dst
 
     for _ in range(a.warmup):
         for _, f in ops:
