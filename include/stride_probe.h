@@ -1,0 +1,31 @@
+/* Methodology probes for the MI355X GEMM design (libstride_probe.so), the gfx950
+ * counterparts of the reference's tools/tc_probe.cu (Q1: mma position invariance,
+ * tools/tc_probe.cu:25-35,106-139) and tools/bench_memread.cu (DRAM read pattern
+ * throughput, tools/bench_memread.cu:20-83). Not part of the GEMM path. */
+#ifndef STRIDE_PROBE_H
+#define STRIDE_PROBE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* One v_mfma_f32_16x16x32_bf16 per tile t: out_t = A_t * B_t + C_t, where A_t is
+ * a 16-row x 32-column bf16 chunk in the packed weight layout (two 16x16 tiles,
+ * 1 KiB), B_t a 32-column chunk of 16 activation lanes in the x layout (1 KiB),
+ * and C_t / out_t fp32 16x16 tiles in the h layout ([16 lanes][16 rows]). */
+int stride_probe_mfma_tiles(const uint16_t* a, const uint16_t* b, const float* c, float* out, int32_t tiles,
+                            void* stream);
+
+/* Streams `bytes` (a multiple of 16) from `buf` with `blocks` workgroups of 256
+ * threads, each thread keeping `unroll` (1, 4, 8 or 16) 16-byte loads in flight,
+ * consecutive threads on consecutive 16-byte words; writes one xor-checksum word
+ * per workgroup to out[blocks]. blocks = 0 picks one workgroup per 64 KiB. */
+int stride_probe_read(const void* buf, int64_t bytes, uint32_t* out, int32_t blocks, int32_t unroll, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -154,6 +154,16 @@ int stride_tc_lm_full(const StrideTcLmFullParams* p, int lane_tiles_per_block, v
  * of n rows and k columns. Depends on (n, k) only. */
 int stride_tc_split_count(int32_t n, int32_t k);
 
+/* Tuning hook, no reference counterpart: force the decode-regime (M <= 128)
+ * kernel configuration `index` (0 .. stride_tc_stream_config_count()-1) for the
+ * calling process, or -1 for the automatic choice. Every configuration computes
+ * identical bits; this only changes speed. A configuration that cannot serve a
+ * launch is ignored for it. */
+int stride_tc_set_stream_config(int32_t index);
+int stride_tc_stream_config_count(void);
+/* Writes (R, LT, WS, WR, U, XL) of configuration `index` into out6. */
+int stride_tc_stream_config(int32_t index, int32_t* out6);
+
 /* Message for the last nonzero return on this thread ("" if none). */
 const char* stride_tc_last_error(void);
 

@@ -85,6 +85,9 @@ EXPORTS = (
     "stride_tc_split_count",
     "stride_tc_last_error",
     "stride_tc_version",
+    "stride_tc_set_stream_config",
+    "stride_tc_stream_config_count",
+    "stride_tc_stream_config",
 )
 
 
@@ -130,6 +133,12 @@ def load(path: str = LIB_PATH) -> C.CDLL:
                  "stride_tc_lm_full", "stride_tc_split_count"):
         getattr(lib, name).restype = C.c_int
     lib.stride_tc_split_count.argtypes = [C.c_int32, C.c_int32]
+    lib.stride_tc_set_stream_config.argtypes = [C.c_int32]
+    lib.stride_tc_set_stream_config.restype = C.c_int
+    lib.stride_tc_stream_config_count.argtypes = []
+    lib.stride_tc_stream_config_count.restype = C.c_int
+    lib.stride_tc_stream_config.argtypes = [C.c_int32, C.POINTER(C.c_int32)]
+    lib.stride_tc_stream_config.restype = C.c_int
     lib.stride_tc_last_error.restype = C.c_char_p
     lib.stride_tc_last_error.argtypes = []
     lib.stride_tc_version.restype = C.c_char_p
@@ -150,3 +159,19 @@ def split_count(n: int, k: int) -> int:
     if s < 0:
         check(s)
     return s
+
+
+def stream_configs():
+    """[(R, LT, WS, WR, U, XL)] of the decode-regime kernel configurations."""
+    lib = load()
+    out = []
+    for i in range(lib.stride_tc_stream_config_count()):
+        buf = (C.c_int32 * 6)()
+        check(lib.stride_tc_stream_config(i, buf))
+        out.append(tuple(buf))
+    return out
+
+
+def set_stream_config(index: int) -> None:
+    """Force a decode-regime configuration (-1 = automatic); results never change."""
+    check(load().stride_tc_set_stream_config(index))

@@ -13,6 +13,8 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 SOURCES = [os.path.join(HERE, "csrc", "tc_gemm.hip")]
 OUT = os.path.join(HERE, "libstride_tc.so")
+PROBE_SOURCES = [os.path.join(HERE, "csrc", "probe.hip")]
+PROBE_OUT = os.path.join(HERE, "libstride_probe.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
     "-O3", "--offload-arch=gfx950", "-std=c++17", "-shared", "-fPIC",
@@ -20,14 +22,21 @@ FLAGS = [
 ]
 
 
-def build(verbose: bool = False) -> str:
-    cmd = [HIPCC, *FLAGS, "-o", OUT, *SOURCES]
+def _hipcc(out: str, sources, verbose: bool) -> None:
+    cmd = [HIPCC, *FLAGS, "-o", out, *sources]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         sys.stderr.write(res.stdout + res.stderr)
-        raise RuntimeError("hipcc failed building libstride_tc.so")
+        raise RuntimeError(f"hipcc failed building {os.path.basename(out)}")
     if verbose:
         print(" ".join(cmd))
+
+
+def build(verbose: bool = False) -> str:
+    """Builds libstride_tc.so (the GEMM library) and libstride_probe.so (the
+    methodology probes)."""
+    _hipcc(OUT, SOURCES, verbose)
+    _hipcc(PROBE_OUT, PROBE_SOURCES, verbose)
     return OUT
 
 

@@ -1,0 +1,210 @@
+// Problem geometry and the epilogues shared by every GEMM kernel family.
+// Epilogues receive one finished 16x16 output tile per matrix in MFMA fragment
+// layout (lane l holds batch lane l%16, rows 4*(l/16)+i) and write it in the
+// reference's output layout; every kernel variant calls the same functions, so
+// the output bits do not depend on which variant ran.
+#pragma once
+
+#include "tc_common.hpp"
+
+namespace stride_tc {
+
+// ---------------------------------------------------------------------------
+// Problem geometry shared by all kernels: up to three row segments (Q, K, V for
+// the fused QKV; one otherwise), all consuming the same activation tiles.
+
+struct Segment {
+  const uint16_t* w[2];  // second matrix used by the paired gate/up GEMM
+  int32_t row_tiles;
+  int32_t splits;
+  int32_t blocks;        // row blocks of this segment in the current launch
+};
+
+struct Geometry {
+  const uint16_t* x;
+  int32_t col_tiles;
+  int32_t rows;
+  int32_t lane_groups;
+  int32_t nseg;
+  Segment seg[3];
+};
+
+// Spread consecutive logical blocks over one XCD: hardware hands workgroup i to
+// XCD i % 8, so logical neighbours (which share weight or activation tiles) are
+// made to land on the same L2. Bijective on [0, n).
+__device__ __forceinline__ int xcd_remap(int i, int n) {
+  const int full = n & ~7;
+  if (i >= full) return i;
+  return (i & 7) * (full >> 3) + (i >> 3);
+}
+
+__device__ __forceinline__ int locate_segment(const Geometry& g, int& rb) {
+  int s = 0;
+  while (s + 1 < g.nseg && rb >= g.seg[s].blocks) {
+    rb -= g.seg[s].blocks;
+    ++s;
+  }
+  return s;
+}
+
+// ---------------------------------------------------------------------------
+// Epilogues. Each receives one finished 16x16 tile y (fragment layout: lane l
+// holds lane l%16, rows 4*(l/16)+i) per matrix and writes it out. They are
+// called by whole wavefronts (QKV and the argmax exchange values across lanes).
+
+struct EpiResidual {  // h <- h + W x   (reference src/kernels_tc.cu:438-501)
+  static constexpr int kMats = 1;
+  static constexpr bool kInitFromOutput = true;
+  struct Out {
+    float* h;
+    int32_t h_tiles;
+  };
+  __device__ static float* at(const Out& o, int rt, int lt, int lane) {
+    return o.h + (static_cast<int64_t>(lt) * o.h_tiles + rt) * kTileElems + (lane & 15) * 16 + (lane >> 4) * 4;
+  }
+  __device__ static f32x4 init(const Out& o, int rt, int lt, int lane) {
+    return *reinterpret_cast<const f32x4*>(at(o, rt, lt, lane));
+  }
+  __device__ static void apply(const Out& o, const Geometry&, int, int rt, int lt, const f32x4* y, int lane) {
+    *reinterpret_cast<f32x4*>(at(o, rt, lt, lane)) = y[0];
+  }
+};
+
+struct EpiLogits {  // logits tiles [rt][lt][16 rows][16 lanes]  (src/kernels_tc.cu:632-655)
+  static constexpr int kMats = 1;
+  static constexpr bool kInitFromOutput = false;
+  struct Out {
+    float* logits;
+  };
+  __device__ static f32x4 init(const Out&, int, int, int) { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+  __device__ static void apply(const Out& o, const Geometry& g, int, int rt, int lt, const f32x4* y, int lane) {
+    float* base = o.logits + (static_cast<int64_t>(rt) * g.lane_groups + lt) * kTileElems + (lane >> 4) * 64 + (lane & 15);
+    base[0] = y[0][0];
+    base[16] = y[0][1];
+    base[32] = y[0][2];
+    base[48] = y[0][3];
+  }
+};
+
+struct EpiGateUp {  // z = bf16(det_silu(W1 x) * (W3 x))  (src/kernels_tc.cu:505-564)
+  static constexpr int kMats = 2;
+  static constexpr bool kInitFromOutput = false;
+  struct Out {
+    uint16_t* z;
+    int32_t z_tiles;
+  };
+  __device__ static f32x4 init(const Out&, int, int, int) { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+  __device__ static void apply(const Out& o, const Geometry&, int, int rt, int lt, const f32x4* y, int lane) {
+    uint32_t b[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float gate = det_silu(y[0][i]);
+      b[i] = bf16_rne(gate * y[1][i]);
+    }
+    u32x2 packed = {b[0] | (b[1] << 16), b[2] | (b[3] << 16)};
+    uint16_t* z = o.z + (static_cast<int64_t>(lt) * o.z_tiles + rt) * kTileElems + (lane & 15) * 16 + (lane >> 4) * 4;
+    *reinterpret_cast<u32x2*>(z) = packed;
+  }
+};
+
+struct EpiArgmax {  // per-lane greedy argmax  (src/kernels_tc.cu:590-630)
+  static constexpr int kMats = 1;
+  static constexpr bool kInitFromOutput = false;
+  struct Out {
+    StrideBestEntry* best;
+    int32_t vocab;
+  };
+  __device__ static f32x4 init(const Out&, int, int, int) { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+  __device__ static void apply(const Out& o, const Geometry& g, int, int rt, int lt, const f32x4* y, int lane) {
+    float bv = f32_of(0xFF800000u);
+    int32_t bi = -1;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int index = rt * 16 + (lane >> 4) * 4 + i;
+      if (index < o.vocab && y[0][i] > bv) {
+        bv = y[0][i];
+        bi = index;
+      }
+    }
+    // Merge the four row groups of this lane column; the merge is the
+    // lexicographic max, so the exchange order does not matter.
+#pragma unroll
+    for (int sh = 16; sh <= 32; sh <<= 1) {
+      const float ov = __shfl_xor(bv, sh);
+      const int32_t oi = __shfl_xor(bi, sh);
+      if (oi >= 0 && (bi < 0 || better_than(ov, oi, bv, bi))) {
+        bv = ov;
+        bi = oi;
+      }
+    }
+    const int j = lt * 16 + (lane & 15);
+    if (lane < 16 && j < g.rows && bi >= 0) best_update(&o.best[j], bv, bi);
+  }
+};
+
+struct EpiQkv {  // RoPE + q store + bf16 KV append  (src/kernels_tc.cu:347-432)
+  static constexpr int kMats = 1;
+  static constexpr bool kInitFromOutput = false;
+  struct Out {
+    float* q_out;
+    int32_t q_stride;
+    int32_t layer;
+    int32_t head_dim;
+    int32_t page_shift;  // log2(tokens per KV page) = log2(group_elems / head_dim)
+    StrideKvRef kv;
+    const float* rope;
+    const int32_t* row_slot;
+    const int32_t* row_pos;
+  };
+  __device__ static f32x4 init(const Out&, int, int, int) { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+  __device__ static uint16_t* kv_row(const Out& o, int which, int head, int slot, int pos) {
+    const StrideKvRef& kv = o.kv;
+    const int64_t block = kv.table[static_cast<int64_t>(slot) * kv.max_blocks + (pos >> o.page_shift)];
+    const int token = pos & ((1 << o.page_shift) - 1);
+    return static_cast<uint16_t*>(kv.arena) + block * kv.block_elems + o.layer * kv.layer_elems + which * kv.which_elems +
+           head * kv.group_elems + static_cast<int64_t>(token) * kv.head_dim;
+  }
+  __device__ static void apply(const Out& o, const Geometry& g, int kind, int rt, int lt, const f32x4* y, int lane) {
+    // Row m (< 8) of the tile pairs with row m + 8: lanes l and l ^ 32.
+    float partner[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) partner[i] = __shfl_xor(y[0][i], 32);
+    if (lane >= 32) return;
+    const int D = o.head_dim;
+    const int tiles_per_head = D / 16;
+    const int head = rt / tiles_per_head;
+    const int d0 = (rt % tiles_per_head) * 8;
+    const int half = D / 2;
+    const int j = lt * 16 + (lane & 15);
+    if (j >= g.rows) return;
+    const int pos = o.row_pos[j];
+    const int slot = o.row_slot[j];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int d = d0 + (lane >> 4) * 4 + i;
+      const float a = y[0][i];
+      const float b = partner[i];
+      if (kind == 2) {
+        uint16_t* dst = kv_row(o, 1, head, slot, pos);
+        dst[d] = static_cast<uint16_t>(bf16_rne(a));
+        dst[d + half] = static_cast<uint16_t>(bf16_rne(b));
+      } else {
+        const float* cs = o.rope + (static_cast<int64_t>(pos) * half + d) * 2;
+        const float co = cs[0], si = cs[1];
+        const float ra = a * co - b * si;
+        const float rb = b * co + a * si;
+        if (kind == 0) {
+          float* q = o.q_out + static_cast<int64_t>(j) * o.q_stride + static_cast<int64_t>(head) * D;
+          q[d] = ra;
+          q[d + half] = rb;
+        } else {
+          uint16_t* dst = kv_row(o, 0, head, slot, pos);
+          dst[d] = static_cast<uint16_t>(bf16_rne(ra));
+          dst[d + half] = static_cast<uint16_t>(bf16_rne(rb));
+        }
+      }
+    }
+  }
+};
+
+}  // namespace stride_tc

@@ -30,471 +30,15 @@
 
 #include <cstdio>
 #include <cstddef>
+#include <algorithm>
 #include <cstring>
 #include <string>
 
-#include "tc_common.hpp"
+#include "tc_epilogue.hpp"
+#include "tc_stream.hpp"
+#include "tc_tile.hpp"
 
 namespace stride_tc {
-
-// ---------------------------------------------------------------------------
-// Problem geometry shared by all kernels: up to three row segments (Q, K, V for
-// the fused QKV; one otherwise), all consuming the same activation tiles.
-
-struct Segment {
-  const uint16_t* w[2];  // second matrix used by the paired gate/up GEMM
-  int32_t row_tiles;
-  int32_t splits;
-  int32_t blocks;        // row blocks of this segment in the current launch
-};
-
-struct Geometry {
-  const uint16_t* x;
-  int32_t col_tiles;
-  int32_t rows;
-  int32_t lane_groups;
-  int32_t nseg;
-  Segment seg[3];
-};
-
-// Spread consecutive logical blocks over one XCD: hardware hands workgroup i to
-// XCD i % 8, so logical neighbours (which share weight or activation tiles) are
-// made to land on the same L2. Bijective on [0, n).
-__device__ __forceinline__ int xcd_remap(int i, int n) {
-  const int full = n & ~7;
-  if (i >= full) return i;
-  return (i & 7) * (full >> 3) + (i >> 3);
-}
-
-__device__ __forceinline__ int locate_segment(const Geometry& g, int& rb) {
-  int s = 0;
-  while (s + 1 < g.nseg && rb >= g.seg[s].blocks) {
-    rb -= g.seg[s].blocks;
-    ++s;
-  }
-  return s;
-}
-
-// ---------------------------------------------------------------------------
-// Epilogues. Each receives one finished 16x16 tile y (fragment layout: lane l
-// holds lane l%16, rows 4*(l/16)+i) per matrix and writes it out. They are
-// called by whole wavefronts (QKV and the argmax exchange values across lanes).
-
-struct EpiResidual {  // h <- h + W x   (reference src/kernels_tc.cu:438-501)
-  static constexpr int kMats = 1;
-  static constexpr bool kInitFromOutput = true;
-  struct Out {
-    float* h;
-    int32_t h_tiles;
-  };
-  __device__ static float* at(const Out& o, int rt, int lt, int lane) {
-    return o.h + (static_cast<int64_t>(lt) * o.h_tiles + rt) * kTileElems + (lane & 15) * 16 + (lane >> 4) * 4;
-  }
-  __device__ static f32x4 init(const Out& o, int rt, int lt, int lane) {
-    return *reinterpret_cast<const f32x4*>(at(o, rt, lt, lane));
-  }
-  __device__ static void apply(const Out& o, const Geometry&, int, int rt, int lt, const f32x4* y, int lane) {
-    *reinterpret_cast<f32x4*>(at(o, rt, lt, lane)) = y[0];
-  }
-};
-
-struct EpiLogits {  // logits tiles [rt][lt][16 rows][16 lanes]  (src/kernels_tc.cu:632-655)
-  static constexpr int kMats = 1;
-  static constexpr bool kInitFromOutput = false;
-  struct Out {
-    float* logits;
-  };
-  __device__ static f32x4 init(const Out&, int, int, int) { return f32x4{0.f, 0.f, 0.f, 0.f}; }
-  __device__ static void apply(const Out& o, const Geometry& g, int, int rt, int lt, const f32x4* y, int lane) {
-    float* base = o.logits + (static_cast<int64_t>(rt) * g.lane_groups + lt) * kTileElems + (lane >> 4) * 64 + (lane & 15);
-    base[0] = y[0][0];
-    base[16] = y[0][1];
-    base[32] = y[0][2];
-    base[48] = y[0][3];
-  }
-};
-
-struct EpiGateUp {  // z = bf16(det_silu(W1 x) * (W3 x))  (src/kernels_tc.cu:505-564)
-  static constexpr int kMats = 2;
-  static constexpr bool kInitFromOutput = false;
-  struct Out {
-    uint16_t* z;
-    int32_t z_tiles;
-  };
-  __device__ static f32x4 init(const Out&, int, int, int) { return f32x4{0.f, 0.f, 0.f, 0.f}; }
-  __device__ static void apply(const Out& o, const Geometry&, int, int rt, int lt, const f32x4* y, int lane) {
-    uint32_t b[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float gate = det_silu(y[0][i]);
-      b[i] = bf16_rne(gate * y[1][i]);
-    }
-    u32x2 packed = {b[0] | (b[1] << 16), b[2] | (b[3] << 16)};
-    uint16_t* z = o.z + (static_cast<int64_t>(lt) * o.z_tiles + rt) * kTileElems + (lane & 15) * 16 + (lane >> 4) * 4;
-    *reinterpret_cast<u32x2*>(z) = packed;
-  }
-};
-
-struct EpiArgmax {  // per-lane greedy argmax  (src/kernels_tc.cu:590-630)
-  static constexpr int kMats = 1;
-  static constexpr bool kInitFromOutput = false;
-  struct Out {
-    StrideBestEntry* best;
-    int32_t vocab;
-  };
-  __device__ static f32x4 init(const Out&, int, int, int) { return f32x4{0.f, 0.f, 0.f, 0.f}; }
-  __device__ static void apply(const Out& o, const Geometry& g, int, int rt, int lt, const f32x4* y, int lane) {
-    float bv = f32_of(0xFF800000u);
-    int32_t bi = -1;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int index = rt * 16 + (lane >> 4) * 4 + i;
-      if (index < o.vocab && y[0][i] > bv) {
-        bv = y[0][i];
-        bi = index;
-      }
-    }
-    // Merge the four row groups of this lane column; the merge is the
-    // lexicographic max, so the exchange order does not matter.
-#pragma unroll
-    for (int sh = 16; sh <= 32; sh <<= 1) {
-      const float ov = __shfl_xor(bv, sh);
-      const int32_t oi = __shfl_xor(bi, sh);
-      if (oi >= 0 && (bi < 0 || better_than(ov, oi, bv, bi))) {
-        bv = ov;
-        bi = oi;
-      }
-    }
-    const int j = lt * 16 + (lane & 15);
-    if (lane < 16 && j < g.rows && bi >= 0) best_update(&o.best[j], bv, bi);
-  }
-};
-
-struct EpiQkv {  // RoPE + q store + bf16 KV append  (src/kernels_tc.cu:347-432)
-  static constexpr int kMats = 1;
-  static constexpr bool kInitFromOutput = false;
-  struct Out {
-    float* q_out;
-    int32_t q_stride;
-    int32_t layer;
-    int32_t head_dim;
-    int32_t page_shift;  // log2(tokens per KV page) = log2(group_elems / head_dim)
-    StrideKvRef kv;
-    const float* rope;
-    const int32_t* row_slot;
-    const int32_t* row_pos;
-  };
-  __device__ static f32x4 init(const Out&, int, int, int) { return f32x4{0.f, 0.f, 0.f, 0.f}; }
-  __device__ static uint16_t* kv_row(const Out& o, int which, int head, int slot, int pos) {
-    const StrideKvRef& kv = o.kv;
-    const int64_t block = kv.table[static_cast<int64_t>(slot) * kv.max_blocks + (pos >> o.page_shift)];
-    const int token = pos & ((1 << o.page_shift) - 1);
-    return static_cast<uint16_t*>(kv.arena) + block * kv.block_elems + o.layer * kv.layer_elems + which * kv.which_elems +
-           head * kv.group_elems + static_cast<int64_t>(token) * kv.head_dim;
-  }
-  __device__ static void apply(const Out& o, const Geometry& g, int kind, int rt, int lt, const f32x4* y, int lane) {
-    // Row m (< 8) of the tile pairs with row m + 8: lanes l and l ^ 32.
-    float partner[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) partner[i] = __shfl_xor(y[0][i], 32);
-    if (lane >= 32) return;
-    const int D = o.head_dim;
-    const int tiles_per_head = D / 16;
-    const int head = rt / tiles_per_head;
-    const int d0 = (rt % tiles_per_head) * 8;
-    const int half = D / 2;
-    const int j = lt * 16 + (lane & 15);
-    if (j >= g.rows) return;
-    const int pos = o.row_pos[j];
-    const int slot = o.row_slot[j];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int d = d0 + (lane >> 4) * 4 + i;
-      const float a = y[0][i];
-      const float b = partner[i];
-      if (kind == 2) {
-        uint16_t* dst = kv_row(o, 1, head, slot, pos);
-        dst[d] = static_cast<uint16_t>(bf16_rne(a));
-        dst[d + half] = static_cast<uint16_t>(bf16_rne(b));
-      } else {
-        const float* cs = o.rope + (static_cast<int64_t>(pos) * half + d) * 2;
-        const float co = cs[0], si = cs[1];
-        const float ra = a * co - b * si;
-        const float rb = b * co + a * si;
-        if (kind == 0) {
-          float* q = o.q_out + static_cast<int64_t>(j) * o.q_stride + static_cast<int64_t>(head) * D;
-          q[d] = ra;
-          q[d + half] = rb;
-        } else {
-          uint16_t* dst = kv_row(o, 0, head, slot, pos);
-          dst[d] = static_cast<uint16_t>(bf16_rne(ra));
-          dst[d + half] = static_cast<uint16_t>(bf16_rne(rb));
-        }
-      }
-    }
-  }
-};
-
-// ---------------------------------------------------------------------------
-// Decode regime: weight streaming with an in-workgroup K split.
-
-template <class Epi, int R, int LT, int WS, int WR, int SMAX>
-__global__ __launch_bounds__(kWave * WS * WR) void k_stream(Geometry g, typename Epi::Out o) {
-  constexpr int M = Epi::kMats;
-  constexpr int U = (LT >= 8 || M * R >= 4) ? 2 : 4;  // chunks in flight per wave
-  constexpr int kPart = SMAX > 1 ? SMAX * WR * M * R * LT * kWave : 1;
-  __shared__ f32x4 part[kPart];
-
-  const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
-  const int ws = wave % WS, wr = wave / WS;
-  const int lgroups = (g.lane_groups + LT - 1) / LT;
-  const int b = xcd_remap(blockIdx.x, gridDim.x);
-  int rb = b / lgroups;
-  const int lt0 = (b % lgroups) * LT;
-  const int si = locate_segment(g, rb);
-  const Segment& sg = g.seg[si];
-  const int rt_first = rb * (WR * R) + wr * R;
-  const int nlt = min(LT, g.lane_groups - lt0);
-  const int chunks = g.col_tiles >> 1;
-  const int splits = sg.splits;
-  const int per = chunks / splits;
-  const int off = frag_offset(lane);
-  const int64_t strip = static_cast<int64_t>(g.col_tiles) * kTileElems;  // elements per row-tile strip
-
-  const char* wp[M][R];
-#pragma unroll
-  for (int m = 0; m < M; ++m)
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int rt = min(rt_first + r, sg.row_tiles - 1);
-      wp[m][r] = reinterpret_cast<const char*>(sg.w[m] + rt * strip) + off;
-    }
-  const char* xp[LT];
-#pragma unroll
-  for (int l = 0; l < LT; ++l) {
-    const int lt = min(lt0 + l, g.lane_groups - 1);
-    xp[l] = reinterpret_cast<const char*>(g.x + lt * strip) + off;
-  }
-
-  for (int s = ws; s < splits; s += WS) {
-    f32x4 acc[M][R][LT];
-#pragma unroll
-    for (int m = 0; m < M; ++m)
-#pragma unroll
-      for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int l = 0; l < LT; ++l) {
-          acc[m][r][l] = f32x4{0.f, 0.f, 0.f, 0.f};
-          if constexpr (Epi::kInitFromOutput) {
-            if (s == 0 && l < nlt && rt_first + r < sg.row_tiles) acc[m][r][l] = Epi::init(o, rt_first + r, lt0 + l, lane);
-          }
-        }
-    const int c1 = (s + 1) * per;
-    int c = s * per;
-    for (; c + U <= c1; c += U) {
-      u32x4 a[U][M][R], bx[U][LT];
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-#pragma unroll
-        for (int m = 0; m < M; ++m)
-#pragma unroll
-          for (int r = 0; r < R; ++r) a[u][m][r] = load16(wp[m][r] + static_cast<int64_t>(c + u) * kChunkBytes);
-#pragma unroll
-        for (int l = 0; l < LT; ++l)
-          if (l < nlt) bx[u][l] = load16(xp[l] + static_cast<int64_t>(c + u) * kChunkBytes);
-      }
-#pragma unroll
-      for (int u = 0; u < U; ++u)
-#pragma unroll
-        for (int l = 0; l < LT; ++l)
-          if (l < nlt) {
-#pragma unroll
-            for (int m = 0; m < M; ++m)
-#pragma unroll
-              for (int r = 0; r < R; ++r) acc[m][r][l] = mfma(a[u][m][r], bx[u][l], acc[m][r][l]);
-          }
-    }
-    for (; c < c1; ++c) {
-      u32x4 a[M][R], bx[LT];
-#pragma unroll
-      for (int m = 0; m < M; ++m)
-#pragma unroll
-        for (int r = 0; r < R; ++r) a[m][r] = load16(wp[m][r] + static_cast<int64_t>(c) * kChunkBytes);
-#pragma unroll
-      for (int l = 0; l < LT; ++l)
-        if (l < nlt) bx[l] = load16(xp[l] + static_cast<int64_t>(c) * kChunkBytes);
-#pragma unroll
-      for (int l = 0; l < LT; ++l)
-        if (l < nlt) {
-#pragma unroll
-          for (int m = 0; m < M; ++m)
-#pragma unroll
-            for (int r = 0; r < R; ++r) acc[m][r][l] = mfma(a[m][r], bx[l], acc[m][r][l]);
-        }
-    }
-
-    if constexpr (SMAX == 1) {
-      // One split: the chain is the result.
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        if (rt_first + r >= sg.row_tiles) continue;
-#pragma unroll
-        for (int l = 0; l < LT; ++l) {
-          if (l >= nlt) continue;
-          f32x4 y[M];
-#pragma unroll
-          for (int m = 0; m < M; ++m) y[m] = acc[m][r][l];
-          Epi::apply(o, g, si, rt_first + r, lt0 + l, y, lane);
-        }
-      }
-    } else {
-#pragma unroll
-      for (int m = 0; m < M; ++m)
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-#pragma unroll
-          for (int l = 0; l < LT; ++l)
-            part[((((s * WR + wr) * M + m) * R + r) * LT + l) * kWave + lane] = acc[m][r][l];
-    }
-  }
-
-  if constexpr (SMAX > 1) {
-    __syncthreads();
-    // Combine the split partials of each tile in ascending split order.
-    for (int t = wave; t < WR * R * LT; t += WS * WR) {
-      const int twr = t / (R * LT), r = (t / LT) % R, l = t % LT;
-      const int rt = rb * (WR * R) + twr * R + r;
-      if (l >= nlt || rt >= sg.row_tiles) continue;
-      f32x4 y[M];
-#pragma unroll
-      for (int m = 0; m < M; ++m) {
-        y[m] = part[((((0 * WR + twr) * M + m) * R + r) * LT + l) * kWave + lane];
-        for (int s = 1; s < splits; ++s) y[m] = y[m] + part[((((s * WR + twr) * M + m) * R + r) * LT + l) * kWave + lane];
-      }
-      Epi::apply(o, g, si, rt, lt0 + l, y, lane);
-    }
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Prefill regime: LDS-staged block GEMM, 4 waves in a 2x2 grid.
-
-template <class Epi, int WRT, int WLT>
-__global__ __launch_bounds__(256) void k_tile(Geometry g, typename Epi::Out o) {
-  constexpr int M = Epi::kMats;
-  constexpr int BR = 2 * WRT, BL = 2 * WLT;
-  constexpr int NB = M * BR + BL;  // 1 KiB blocks staged per chunk
-  static_assert(NB % 4 == 0, "staging assumes whole rounds of 256 x 16 B");
-  constexpr int ROUNDS = NB / 4;
-  __shared__ u32x4 stage[2][NB * kWave];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int wr = wave >> 1, wl = wave & 1;
-  const int lblocks = (g.lane_groups + BL - 1) / BL;
-  const int b = xcd_remap(blockIdx.x, gridDim.x);
-  int rb = b / lblocks;
-  const int lt0 = (b % lblocks) * BL;
-  const int si = locate_segment(g, rb);
-  const Segment& sg = g.seg[si];
-  const int rt0 = rb * BR;
-  const int chunks = g.col_tiles >> 1;
-  const int per = chunks / sg.splits;
-  const int64_t strip = static_cast<int64_t>(g.col_tiles) * kTileElems;
-
-  // Staging assignment: thread tid moves piece P = q*256 + tid of each chunk.
-  const char* src[ROUNDS];
-  int dst[ROUNDS];
-#pragma unroll
-  for (int q = 0; q < ROUNDS; ++q) {
-    const int P = q * 256 + tid;
-    const int blk = P >> 6, j = P & 63;
-    const uint16_t* base;
-    if (blk < M * BR) {
-      const int m = blk / BR;
-      const int rt = min(rt0 + blk % BR, sg.row_tiles - 1);
-      base = sg.w[m] + rt * strip;
-    } else {
-      const int lt = min(lt0 + blk - M * BR, g.lane_groups - 1);
-      base = g.x + lt * strip;
-    }
-    src[q] = reinterpret_cast<const char*>(base) + j * 16;
-    dst[q] = blk * kWave + frag_lane_of_piece(j);
-  }
-
-  u32x4 pre[ROUNDS];
-#pragma unroll
-  for (int q = 0; q < ROUNDS; ++q) pre[q] = load16(src[q]);
-#pragma unroll
-  for (int q = 0; q < ROUNDS; ++q) stage[0][dst[q]] = pre[q];
-  __syncthreads();
-
-  f32x4 acc[M][WRT][WLT], y[M][WRT][WLT];
-  for (int c = 0; c < chunks; ++c) {
-    const int buf = c & 1;
-    if (c + 1 < chunks) {
-#pragma unroll
-      for (int q = 0; q < ROUNDS; ++q) pre[q] = load16(src[q] + static_cast<int64_t>(c + 1) * kChunkBytes);
-    }
-    const int s = c / per;
-    if (c == s * per) {
-#pragma unroll
-      for (int m = 0; m < M; ++m)
-#pragma unroll
-        for (int r = 0; r < WRT; ++r)
-#pragma unroll
-          for (int l = 0; l < WLT; ++l) {
-            acc[m][r][l] = f32x4{0.f, 0.f, 0.f, 0.f};
-            if constexpr (Epi::kInitFromOutput) {
-              const int rt = rt0 + wr * WRT + r, lt = lt0 + wl * WLT + l;
-              if (s == 0 && rt < sg.row_tiles && lt < g.lane_groups) acc[m][r][l] = Epi::init(o, rt, lt, lane);
-            }
-          }
-    }
-    u32x4 af[M][WRT], bf[WLT];
-#pragma unroll
-    for (int m = 0; m < M; ++m)
-#pragma unroll
-      for (int r = 0; r < WRT; ++r) af[m][r] = stage[buf][(m * BR + wr * WRT + r) * kWave + lane];
-#pragma unroll
-    for (int l = 0; l < WLT; ++l) bf[l] = stage[buf][(M * BR + wl * WLT + l) * kWave + lane];
-#pragma unroll
-    for (int l = 0; l < WLT; ++l)
-#pragma unroll
-      for (int m = 0; m < M; ++m)
-#pragma unroll
-        for (int r = 0; r < WRT; ++r) acc[m][r][l] = mfma(af[m][r], bf[l], acc[m][r][l]);
-    if (c + 1 == (s + 1) * per) {
-#pragma unroll
-      for (int m = 0; m < M; ++m)
-#pragma unroll
-        for (int r = 0; r < WRT; ++r)
-#pragma unroll
-          for (int l = 0; l < WLT; ++l) y[m][r][l] = s == 0 ? acc[m][r][l] : y[m][r][l] + acc[m][r][l];
-    }
-    if (c + 1 < chunks) {
-#pragma unroll
-      for (int q = 0; q < ROUNDS; ++q) stage[buf ^ 1][dst[q]] = pre[q];
-    }
-    __syncthreads();
-  }
-
-#pragma unroll
-  for (int r = 0; r < WRT; ++r) {
-    const int rt = rt0 + wr * WRT + r;
-    if (rt >= sg.row_tiles) continue;
-#pragma unroll
-    for (int l = 0; l < WLT; ++l) {
-      const int lt = lt0 + wl * WLT + l;
-      if (lt >= g.lane_groups) continue;
-      f32x4 yy[M];
-#pragma unroll
-      for (int m = 0; m < M; ++m) yy[m] = y[m][r][l];
-      Epi::apply(o, g, si, rt, lt, yy, lane);
-    }
-  }
-}
 
 // ---------------------------------------------------------------------------
 // Host side: split rule, validation, launch selection.
@@ -536,23 +80,97 @@ bool mat_ok(const StrideGemmMat& m, const char* name, std::string& why) {
   return true;
 }
 
-template <class Epi, int R, int LT, int WS, int WR, int SMAX>
-int launch_stream(Geometry g, const typename Epi::Out& o, hipStream_t st) {
+// Decode-regime configurations of k_stream: (R row tiles per wave, LT lane tiles,
+// WS split waves, WR row waves, U chunks per batch, XL x staged in LDS). Which
+// one runs never changes results: all evaluate the same chunk order and the same
+// split combine. The table is indexed by stride_tc_set_stream_config() for tuning
+// sweeps and by pick_decode() otherwise.
+#define STRIDE_TC_DECODE_CONFIGS(S) \
+  S(0, 1, 1, 8, 1, 8, false)          \
+  S(1, 1, 1, 8, 1, 4, false)          \
+  S(2, 1, 1, 2, 4, 8, false)          \
+  S(3, 1, 1, 1, 8, 8, false)          \
+  S(4, 1, 1, 1, 4, 8, false)          \
+  S(5, 1, 2, 8, 1, 8, false)          \
+  S(6, 1, 2, 2, 4, 8, false)          \
+  S(7, 1, 2, 1, 8, 8, false)          \
+  S(8, 1, 4, 8, 1, 4, false)          \
+  S(9, 2, 4, 8, 1, 2, false)          \
+  S(10, 1, 4, 2, 4, 4, false)         \
+  S(11, 1, 4, 2, 4, 2, true)          \
+  S(12, 1, 4, 1, 8, 4, false)         \
+  S(13, 2, 4, 1, 8, 2, true)          \
+  S(14, 1, 8, 8, 1, 2, false)         \
+  S(15, 2, 8, 8, 1, 2, false)         \
+  S(16, 1, 8, 1, 8, 2, true)          \
+  S(17, 1, 8, 1, 8, 2, false)         \
+  S(18, 1, 1, 16, 1, 4, false)        \
+  S(19, 1, 1, 16, 1, 8, false)        \
+  S(20, 1, 2, 16, 1, 4, false)        \
+  S(21, 1, 4, 16, 1, 2, false)        \
+  S(22, 1, 2, 4, 2, 4, false)         \
+  S(23, 1, 1, 4, 2, 8, false)         \
+  S(24, 1, 4, 4, 2, 4, false)         \
+  S(25, 1, 2, 16, 1, 2, false)        \
+  S(26, 1, 1, 16, 1, 2, false)
+
+struct DecodeCfg {
+  int r, lt, ws, wr, u;
+  bool xl;
+};
+
+#define STRIDE_TC_ROW(i, R, LT, WS, WR, U, XL) {R, LT, WS, WR, U, XL},
+constexpr DecodeCfg kDecodeCfgs[] = {STRIDE_TC_DECODE_CONFIGS(STRIDE_TC_ROW)};
+#undef STRIDE_TC_ROW
+constexpr int kNumDecodeCfgs = sizeof(kDecodeCfgs) / sizeof(kDecodeCfgs[0]);
+
+int g_forced_cfg = -1;
+
+template <class Epi, int R, int LT, int WS, int WR, int U, bool XL>
+void launch_stream(Geometry g, const typename Epi::Out& o, hipStream_t st) {
   int blocks = 0;
   for (int i = 0; i < g.nseg; ++i) {
     g.seg[i].blocks = (g.seg[i].row_tiles + WR * R - 1) / (WR * R);
     blocks += g.seg[i].blocks;
   }
   blocks *= (g.lane_groups + LT - 1) / LT;
-  hipLaunchKernelGGL((k_stream<Epi, R, LT, WS, WR, SMAX>), dim3(blocks), dim3(kWave * WS * WR), 0, st, g, o);
-  return 0;
+  hipLaunchKernelGGL((k_stream<Epi, R, LT, WS, WR, U, XL>), dim3(blocks), dim3(kWave * WS * WR), 0, st, g, o);
 }
 
-template <class Epi, int LT>
-int dispatch_stream_lt(const Geometry& g, const typename Epi::Out& o, int smax, hipStream_t st) {
-  if (smax == 1) return launch_stream<Epi, 1, LT, 1, 4, 1>(g, o, st);
-  if (smax == 2) return launch_stream<Epi, 1, LT, 2, 2, 2>(g, o, st);
-  return launch_stream<Epi, 1, LT, 4, 1, 8>(g, o, st);
+template <class Epi>
+void launch_decode_cfg(int idx, const Geometry& g, const typename Epi::Out& o, hipStream_t st) {
+  switch (idx) {
+#define STRIDE_TC_CASE(i, R, LT, WS, WR, U, XL) \
+  case i:                                       \
+    launch_stream<Epi, R, LT, WS, WR, U, XL>(g, o, st); \
+    break;
+    STRIDE_TC_DECODE_CONFIGS(STRIDE_TC_CASE)
+#undef STRIDE_TC_CASE
+    default:
+      break;
+  }
+}
+
+// Can configuration c serve this launch?
+bool decode_cfg_fits(const DecodeCfg& c, Geometry g, int smax, int mats) {
+  const int u = c.u / mats > 0 ? c.u / mats : 1;
+  if (c.ws < smax) return false;
+  if (c.xl && (u * c.lt) % c.wr == 0) {
+    const int chunks = g.col_tiles >> 1;
+    for (int i = 0; i < g.nseg; ++i)
+      if (g.seg[i].splits != c.ws || (chunks / g.seg[i].splits) % u != 0) return false;
+  }
+  return true;
+}
+
+// Default choice by lane-tile count and split count (from measured sweeps).
+int pick_decode(int T, int smax, int mats) {
+  (void)mats;
+  if (smax > 8) return T <= 1 ? 18 : (T <= 2 ? 20 : 21);
+  if (T <= 1) return smax == 1 ? 4 : 1;
+  if (T <= 2) return smax == 1 ? 7 : 5;
+  if (T <= 4) return smax == 1 ? 13 : (smax == 2 ? 9 : 8);
+  return smax == 1 ? 16 : (smax == 2 ? 10 : 8);
 }
 
 template <class Epi, int WRT, int WLT>
@@ -575,15 +193,18 @@ int run(Geometry g, const typename Epi::Out& o, hipStream_t st) {
   if (g.rows == 0) return 0;
   int smax = 1;
   for (int i = 0; i < g.nseg; ++i) {
-    if (g.seg[i].splits > 8) return fail(STRIDE_TC_EINVAL, "split count above 8");
+    if (g.seg[i].splits > 16) return fail(STRIDE_TC_EINVAL, "split count above 16");
     smax = g.seg[i].splits > smax ? g.seg[i].splits : smax;
   }
   const int T = g.lane_groups;
   if (T <= kStreamMaxLaneTiles) {
-    if (T <= 1) dispatch_stream_lt<Epi, 1>(g, o, smax, st);
-    else if (T <= 2) dispatch_stream_lt<Epi, 2>(g, o, smax, st);
-    else if (T <= 4) dispatch_stream_lt<Epi, 4>(g, o, smax, st);
-    else dispatch_stream_lt<Epi, 8>(g, o, smax, st);
+    int idx = pick_decode(T, smax, Epi::kMats);
+    if (g_forced_cfg >= 0 && decode_cfg_fits(kDecodeCfgs[g_forced_cfg], g, smax, Epi::kMats)) idx = g_forced_cfg;
+    if (!decode_cfg_fits(kDecodeCfgs[idx], g, smax, Epi::kMats)) {
+      // fall back to a register-only in-workgroup configuration with a wave per split
+      idx = smax == 1 ? 3 : (smax == 2 ? 2 : (smax <= 8 ? 0 : 18));
+    }
+    launch_decode_cfg<Epi>(idx, g, o, st);
   } else {
     if constexpr (Epi::kMats == 2) launch_tile<Epi, 2, 4>(g, o, st);
     else launch_tile<Epi, 4, 4>(g, o, st);
@@ -624,6 +245,26 @@ static_assert(sizeof(StrideTcLmGreedyParams) == 56, "TcLmGreedyParams layout");
 static_assert(sizeof(StrideTcLmFullParams) == 48, "TcLmFullParams layout");
 
 extern "C" {
+
+int stride_tc_set_stream_config(int32_t index) {
+  if (index < -1 || index >= kNumDecodeCfgs) return fail(STRIDE_TC_EINVAL, "decode config index out of range");
+  g_forced_cfg = index;
+  return 0;
+}
+
+int stride_tc_stream_config_count(void) { return kNumDecodeCfgs; }
+
+int stride_tc_stream_config(int32_t index, int32_t* out6) {
+  if (index < 0 || index >= kNumDecodeCfgs || !out6) return fail(STRIDE_TC_EINVAL, "decode config index out of range");
+  const DecodeCfg& c = kDecodeCfgs[index];
+  out6[0] = c.r;
+  out6[1] = c.lt;
+  out6[2] = c.ws;
+  out6[3] = c.wr;
+  out6[4] = c.u;
+  out6[5] = c.xl ? 1 : 0;
+  return 0;
+}
 
 int stride_tc_split_count(int32_t n, int32_t k) {
   if (n <= 0 || k <= 0 || k % kChunkCols != 0) return fail(-1, "split_count: need n > 0 and k a positive multiple of 32"), -1;

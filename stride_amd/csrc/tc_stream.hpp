@@ -1,0 +1,256 @@
+// Decode-regime kernel (at most 8 lane tiles, M <= 128): weight streaming.
+//
+// Workgroup = WS x WR wavefronts. The WS "split waves" each own one K split
+// (WS >= the matrix's split count S; waves past S idle), so all splits of a row
+// tile run concurrently. The WR "row waves" of one split each own R row tiles,
+// so a workgroup covers WR*R row tiles and LT lane tiles. Each wave streams its
+// weight chunks straight from HBM into registers (16-byte loads, one 1 KiB chunk
+// per wave instruction), double-buffered U chunks at a time. Activation chunks
+// come either straight from L2 (XL = false) or, with XL = true, are staged once
+// per split group into LDS and shared by its WR row waves, which cuts the L2
+// traffic of x by WR*R when many lane tiles are live.
+//
+// The S split partials are combined in ascending split order through one LDS
+// tile buffer: split 0 stores, then split 1 adds, then split 2, ... with a
+// barrier between steps, which evaluates ((c0 + c1) + c2) + ... exactly as the
+// prefill kernel does in registers.
+#pragma once
+
+#include "tc_epilogue.hpp"
+
+namespace stride_tc {
+
+template <class Epi, int R, int LT, int WS, int WR, int UC, bool XLC>
+__global__ __launch_bounds__(kWave * WS * WR) void k_stream(Geometry g, typename Epi::Out o) {
+  constexpr int M = Epi::kMats;
+  // UC counts weight chunks in flight per batch; a paired GEMM loads M chunks per step.
+  constexpr int U = UC / M > 0 ? UC / M : 1;
+  // x staging needs each batch to split evenly over the row waves of a split group.
+  constexpr bool XL = XLC && (U * LT) % WR == 0;
+  constexpr int kY = WS > 1 ? WR * M * R * LT * kWave : 1;           // combine buffer (f32x4 slots)
+  constexpr int kX = XL ? WS * 2 * U * LT * kWave : 1;                // x staging (u32x4 slots)
+  constexpr int kXPieces = U * LT * kWave;                            // 16-byte pieces per x batch
+  constexpr int kXPer = XL ? kXPieces / (WR * kWave) : 1;
+  // The x staging ring is dead once the K loop ends, so the combine buffer
+  // reuses the same LDS.
+  constexpr int kSlots = kY > kX ? kY : kX;
+  __shared__ u32x4 smem[kSlots];
+  f32x4* ybuf = reinterpret_cast<f32x4*>(smem);
+  u32x4* xs = smem;
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int ws = wave % WS, wr = wave / WS;
+  const int lgroups = (g.lane_groups + LT - 1) / LT;
+  const int b = xcd_remap(blockIdx.x, gridDim.x);
+  int rb = b / lgroups;
+  const int lt0 = (b % lgroups) * LT;
+  const int si = locate_segment(g, rb);
+  const Segment& sg = g.seg[si];
+  const int rt_first = rb * (WR * R) + wr * R;
+  const int nlt = min(LT, g.lane_groups - lt0);
+  const int chunks = g.col_tiles >> 1;
+  const int splits = sg.splits;
+  const int per = chunks / splits;
+  const int off = frag_offset(lane);
+  const int64_t strip = static_cast<int64_t>(g.col_tiles) * kTileElems;
+  const bool active = ws < splits;
+
+  const char* wp[M][R];
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int rt = min(rt_first + r, sg.row_tiles - 1);
+      wp[m][r] = reinterpret_cast<const char*>(sg.w[m] + rt * strip) + off;
+    }
+  const char* xp[LT];
+#pragma unroll
+  for (int l = 0; l < LT; ++l) {
+    const int lt = min(lt0 + l, g.lane_groups - 1);
+    xp[l] = reinterpret_cast<const char*>(g.x + lt * strip) + off;
+  }
+  // XL staging: thread (wr, lane) of split group ws moves pieces P = i*WR*64 + wr*64 + lane
+  // of each batch; piece P is (chunk u, lane tile l, 16-byte slot j).
+  const char* xsrc[kXPer];
+  int xdst[kXPer];
+  if constexpr (XL) {
+#pragma unroll
+    for (int i = 0; i < kXPer; ++i) {
+      const int P = (i * WR + wr) * kWave + lane;
+      const int u = P / (LT * kWave), l = (P / kWave) % LT, j = P % kWave;
+      const int lt = min(lt0 + l, g.lane_groups - 1);
+      xsrc[i] = reinterpret_cast<const char*>(g.x + lt * strip) + static_cast<int64_t>(u) * kChunkBytes + j * 16;
+      xdst[i] = (u * LT + l) * kWave + frag_lane_of_piece(j);
+    }
+  }
+
+  f32x4 acc[M][R][LT];
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int l = 0; l < LT; ++l) {
+        acc[m][r][l] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if constexpr (Epi::kInitFromOutput) {
+          if (ws == 0 && l < nlt && rt_first + r < sg.row_tiles) acc[m][r][l] = Epi::init(o, rt_first + r, lt0 + l, lane);
+        }
+      }
+
+  // Chunk range of this wave's split (idle waves of a WG with fewer splits run an
+  // empty range but still take part in the barriers).
+  const int c0 = active ? ws * per : 0;
+  const int c1 = active ? c0 + per : 0;
+  const int nbatch = (c1 - c0) / U;
+  const int cb = c0 + nbatch * U;  // batched range [c0, cb), then single chunks up to c1
+
+  u32x4 a0[U][M][R], a1[U][M][R];
+  u32x4 b0[XL ? 1 : U][LT], b1[XL ? 1 : U][LT];
+  u32x4 xr[kXPer];
+  const int xbase = ws * 2 * U * LT * kWave;
+
+  auto load_w = [&](u32x4 (&a)[U][M][R], int c) {
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int r = 0; r < R; ++r) a[u][m][r] = load16(wp[m][r] + static_cast<int64_t>(c + u) * kChunkBytes);
+  };
+  auto load_x = [&](u32x4 (&bx)[XL ? 1 : U][LT], int c) {
+    if constexpr (!XL) {
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int l = 0; l < LT; ++l) bx[u][l] = load16(xp[l] + static_cast<int64_t>(c + u) * kChunkBytes);
+    }
+  };
+  auto fetch_xl = [&](int c) {
+    if constexpr (XL) {
+#pragma unroll
+      for (int i = 0; i < kXPer; ++i) xr[i] = load16(xsrc[i] + static_cast<int64_t>(c) * kChunkBytes);
+    }
+  };
+  auto store_xl = [&](int buf) {
+    if constexpr (XL) {
+#pragma unroll
+      for (int i = 0; i < kXPer; ++i) xs[xbase + buf * U * LT * kWave + xdst[i]] = xr[i];
+    }
+  };
+  auto mma = [&](const u32x4 (&a)[U][M][R], const u32x4 (&bx)[XL ? 1 : U][LT], int buf) {
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int l = 0; l < LT; ++l) {
+        // Lane tiles past the live ones read a clamped (valid) tile; their
+        // results are discarded. Keeping this loop branch-free lets the compiler
+        // wait only for the loads each MFMA needs.
+        u32x4 bv;
+        if constexpr (XL) bv = xs[xbase + (buf * U * LT + u * LT + l) * kWave + lane];
+        else bv = bx[u][l];
+#pragma unroll
+        for (int m = 0; m < M; ++m)
+#pragma unroll
+          for (int r = 0; r < R; ++r) acc[m][r][l] = mfma(a[u][m][r], bv, acc[m][r][l]);
+      }
+  };
+
+  if constexpr (XL) {
+    // The host only selects x staging when every split group is active
+    // (WS == S for all segments) and U divides the split length.
+    const int nb = per / U;
+    fetch_xl(c0);
+    store_xl(0);
+    load_w(a0, c0);
+    __syncthreads();
+    for (int i = 0; i < nb; ++i) {
+      const int buf = i & 1;
+      const bool more = i + 1 < nb;
+      if (more) fetch_xl(c0 + (i + 1) * U);
+      if ((i & 1) == 0) {
+        if (more) load_w(a1, c0 + (i + 1) * U);
+        mma(a0, b0, buf);
+      } else {
+        if (more) load_w(a0, c0 + (i + 1) * U);
+        mma(a1, b1, buf);
+      }
+      if (more) store_xl(buf ^ 1);
+      __syncthreads();
+    }
+  } else {
+    if (nbatch > 0) {
+      load_w(a0, c0);
+      load_x(b0, c0);
+      int c = c0;
+      for (;;) {
+        if (c + U < cb) {
+          load_w(a1, c + U);
+          load_x(b1, c + U);
+        }
+        mma(a0, b0, 0);
+        c += U;
+        if (c >= cb) break;
+        if (c + U < cb) {
+          load_w(a0, c + U);
+          load_x(b0, c + U);
+        }
+        mma(a1, b1, 0);
+        c += U;
+        if (c >= cb) break;
+      }
+    }
+    for (int c = cb; c < c1; ++c) {  // tail when U does not divide the split
+#pragma unroll
+      for (int l = 0; l < LT; ++l) {
+        const u32x4 bv = load16(xp[l] + static_cast<int64_t>(c) * kChunkBytes);
+#pragma unroll
+        for (int m = 0; m < M; ++m)
+#pragma unroll
+          for (int r = 0; r < R; ++r) acc[m][r][l] = mfma(load16(wp[m][r] + static_cast<int64_t>(c) * kChunkBytes), bv, acc[m][r][l]);
+      }
+    }
+  }
+
+  if constexpr (WS == 1) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if (rt_first + r >= sg.row_tiles) continue;
+#pragma unroll
+      for (int l = 0; l < LT; ++l) {
+        if (l >= nlt) continue;
+        f32x4 y[M];
+#pragma unroll
+        for (int m = 0; m < M; ++m) y[m] = acc[m][r][l];
+        Epi::apply(o, g, si, rt_first + r, lt0 + l, y, lane);
+      }
+    }
+  } else {
+    // Ordered combine: y = c0, then y = y + c1, y = y + c2, ...
+    for (int s = 0; s < splits; ++s) {
+      if (ws == s) {
+#pragma unroll
+        for (int m = 0; m < M; ++m)
+#pragma unroll
+          for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int l = 0; l < LT; ++l) {
+              f32x4& y = ybuf[(((wr * M + m) * R + r) * LT + l) * kWave + lane];
+              y = s == 0 ? acc[m][r][l] : y + acc[m][r][l];
+            }
+      }
+      __syncthreads();
+    }
+    for (int t = wave; t < WR * R * LT; t += WS * WR) {
+      const int twr = t / (R * LT), r = (t / LT) % R, l = t % LT;
+      const int rt = rb * (WR * R) + twr * R + r;
+      if (l >= nlt || rt >= sg.row_tiles) continue;
+      f32x4 y[M];
+#pragma unroll
+      for (int m = 0; m < M; ++m) y[m] = ybuf[(((twr * M + m) * R + r) * LT + l) * kWave + lane];
+      Epi::apply(o, g, si, rt, lt0 + l, y, lane);
+    }
+  }
+}
+
+}  // namespace stride_tc

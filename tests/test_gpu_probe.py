@@ -1,0 +1,61 @@
+"""Methodology probes on the GPU.
+
+MFMA position invariance (the gfx950 counterpart of the reference's tc_probe Q1,
+tools/tc_probe.cu:106-139, reports/g3/tc_probe.txt:1): permuting the rows of A
+(weights) and the lanes of B (activations) inside a tile, with C permuted the same
+way, must permute the v_mfma_f32_16x16x32_bf16 output element for element, bit for
+bit. This is the hardware fact the whole batch-invariance design rests on: an
+output element's bits depend only on its own row, lane and K chunk, never on where
+in the tile that row or lane sits.
+"""
+import numpy as np
+import pytest
+import torch
+
+from stride_amd import probe
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def test_mfma_position_invariance():
+    tiles = 4096
+    g = torch.Generator(device=DEV).manual_seed(3)
+    # A chunk: [t][2 col tiles][16 rows][16 cols]; B chunk: [t][2][16 lanes][16 cols]; C: [t][16 lanes][16 rows]
+    a = torch.randn(tiles, 2, 16, 16, generator=g, device=DEV).to(torch.bfloat16)
+    b = torch.randn(tiles, 2, 16, 16, generator=g, device=DEV).to(torch.bfloat16)
+    c = torch.randn(tiles, 16, 16, generator=g, device=DEV)
+    out = torch.empty_like(c)
+    probe.mfma_tiles(a.view(torch.int16), b.view(torch.int16), c, out, stream())
+    # float64 reference: out[t][n][m] = c[t][n][m] + sum_k A[t][m][k] B[t][n][k]
+    A = a.double().permute(0, 2, 1, 3).reshape(tiles, 16, 32)
+    B = b.double().permute(0, 2, 1, 3).reshape(tiles, 16, 32)
+    ref = c.double() + torch.einsum("tmk,tnk->tnm", A, B)
+    assert torch.allclose(out.double(), ref, atol=1e-5, rtol=1e-5)
+    rp = torch.stack([torch.randperm(16, generator=g, device=DEV) for _ in range(tiles)])
+    lp = torch.stack([torch.randperm(16, generator=g, device=DEV) for _ in range(tiles)])
+    t = torch.arange(tiles, device=DEV)[:, None]
+    ap = a[t, :, rp].permute(0, 2, 1, 3).contiguous()          # rows permuted
+    bp = b[t, :, lp].permute(0, 2, 1, 3).contiguous()          # lanes permuted
+    cp = c[t, lp][t[:, :, None], torch.arange(16, device=DEV)[None, :, None], rp[:, None, :]].contiguous()
+    outp = torch.empty_like(c)
+    probe.mfma_tiles(ap.view(torch.int16), bp.view(torch.int16), cp, outp, stream())
+    expect = out[t, lp][t[:, :, None], torch.arange(16, device=DEV)[None, :, None], rp[:, None, :]]
+    same = int((outp.view(torch.int32) == expect.contiguous().view(torch.int32)).sum())
+    print(f"MFMA row/lane permutation: {same} / {outp.numel()} elements bit-identical", flush=True)
+    assert same == outp.numel()
+
+
+def test_read_probe_checksum():
+    n = 1 << 22  # 16 MiB of int32
+    buf = torch.randint(-2**31, 2**31 - 1, (n,), dtype=torch.int32, device=DEV)
+    want = np.bitwise_xor.reduce(buf.cpu().numpy().view(np.uint32))
+    for unroll in (1, 4, 8, 16):
+        out = torch.zeros(1024, dtype=torch.int32, device=DEV)
+        probe.read(buf, out, 1024, unroll, stream())
+        got = np.bitwise_xor.reduce(out.cpu().numpy().view(np.uint32))
+        assert got == want, unroll
