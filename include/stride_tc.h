@@ -161,6 +161,9 @@ int stride_tc_split_count(int32_t n, int32_t k);
  * launch is ignored for it. */
 int stride_tc_set_stream_config(int32_t index);
 int stride_tc_stream_config_count(void);
+/* Configuration used by the last launch in this process (-2: the prefill
+ * kernel, -1: none yet). */
+int stride_tc_last_stream_config(void);
 /* Writes (R, LT, WS, WR, U, XL) of configuration `index` into out6. */
 int stride_tc_stream_config(int32_t index, int32_t* out6);
 

@@ -88,6 +88,7 @@ EXPORTS = (
     "stride_tc_set_stream_config",
     "stride_tc_stream_config_count",
     "stride_tc_stream_config",
+    "stride_tc_last_stream_config",
 )
 
 
@@ -139,6 +140,8 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     lib.stride_tc_stream_config_count.restype = C.c_int
     lib.stride_tc_stream_config.argtypes = [C.c_int32, C.POINTER(C.c_int32)]
     lib.stride_tc_stream_config.restype = C.c_int
+    lib.stride_tc_last_stream_config.argtypes = []
+    lib.stride_tc_last_stream_config.restype = C.c_int
     lib.stride_tc_last_error.restype = C.c_char_p
     lib.stride_tc_last_error.argtypes = []
     lib.stride_tc_version.restype = C.c_char_p
@@ -175,3 +178,8 @@ def stream_configs():
 def set_stream_config(index: int) -> None:
     """Force a decode-regime configuration (-1 = automatic); results never change."""
     check(load().stride_tc_set_stream_config(index))
+
+
+def last_stream_config() -> int:
+    """Configuration index the last launch used (-2 = prefill kernel)."""
+    return load().stride_tc_last_stream_config()

@@ -112,7 +112,16 @@ bool mat_ok(const StrideGemmMat& m, const char* name, std::string& why) {
   S(23, 1, 1, 4, 2, 8, false)         \
   S(24, 1, 4, 4, 2, 4, false)         \
   S(25, 1, 2, 16, 1, 2, false)        \
-  S(26, 1, 1, 16, 1, 2, false)
+  S(26, 1, 1, 16, 1, 2, false)        \
+  S(27, 2, 4, 8, 1, 4, false)         \
+  S(28, 2, 8, 8, 1, 1, false)         \
+  S(29, 4, 4, 8, 1, 1, false)         \
+  S(30, 4, 8, 8, 1, 1, false)         \
+  S(31, 2, 8, 8, 2, 1, true)          \
+  S(32, 1, 8, 8, 2, 1, true)          \
+  S(33, 2, 2, 8, 1, 4, false)         \
+  S(34, 1, 1, 8, 2, 8, false)         \
+  S(35, 2, 1, 8, 1, 8, false)
 
 struct DecodeCfg {
   int r, lt, ws, wr, u;
@@ -125,6 +134,7 @@ constexpr DecodeCfg kDecodeCfgs[] = {STRIDE_TC_DECODE_CONFIGS(STRIDE_TC_ROW)};
 constexpr int kNumDecodeCfgs = sizeof(kDecodeCfgs) / sizeof(kDecodeCfgs[0]);
 
 int g_forced_cfg = -1;
+int g_last_cfg = -1;  // configuration of the last decode-regime launch (-2: prefill kernel)
 
 template <class Epi, int R, int LT, int WS, int WR, int U, bool XL>
 void launch_stream(Geometry g, const typename Epi::Out& o, hipStream_t st) {
@@ -163,14 +173,15 @@ bool decode_cfg_fits(const DecodeCfg& c, Geometry g, int smax, int mats) {
   return true;
 }
 
-// Default choice by lane-tile count and split count (from measured sweeps).
-int pick_decode(int T, int smax, int mats) {
+// Default choice by lane-tile count, split count and segment count, from
+// measured sweeps on MI355X (HIP-graph timing, weights rotated past the MALL).
+int pick_decode(int T, int smax, int mats, int nseg) {
   (void)mats;
   if (smax > 8) return T <= 1 ? 18 : (T <= 2 ? 20 : 21);
-  if (T <= 1) return smax == 1 ? 4 : 1;
-  if (T <= 2) return smax == 1 ? 7 : 5;
-  if (T <= 4) return smax == 1 ? 13 : (smax == 2 ? 9 : 8);
-  return smax == 1 ? 16 : (smax == 2 ? 10 : 8);
+  if (T <= 1) return smax == 1 ? 4 : (smax == 2 ? 1 : 0);
+  if (T <= 2) return smax == 1 ? 7 : (smax == 2 ? 22 : 1);
+  if (T <= 4) return smax == 1 ? 13 : (smax == 2 ? 27 : (nseg == 3 ? 33 : 5));
+  return smax == 1 ? 16 : (smax == 2 ? 10 : (nseg == 3 ? 9 : 33));
 }
 
 template <class Epi, int WRT, int WLT>
@@ -198,14 +209,16 @@ int run(Geometry g, const typename Epi::Out& o, hipStream_t st) {
   }
   const int T = g.lane_groups;
   if (T <= kStreamMaxLaneTiles) {
-    int idx = pick_decode(T, smax, Epi::kMats);
+    int idx = pick_decode(T, smax, Epi::kMats, g.nseg);
     if (g_forced_cfg >= 0 && decode_cfg_fits(kDecodeCfgs[g_forced_cfg], g, smax, Epi::kMats)) idx = g_forced_cfg;
     if (!decode_cfg_fits(kDecodeCfgs[idx], g, smax, Epi::kMats)) {
       // fall back to a register-only in-workgroup configuration with a wave per split
       idx = smax == 1 ? 3 : (smax == 2 ? 2 : (smax <= 8 ? 0 : 18));
     }
+    g_last_cfg = idx;
     launch_decode_cfg<Epi>(idx, g, o, st);
   } else {
+    g_last_cfg = -2;
     if constexpr (Epi::kMats == 2) launch_tile<Epi, 2, 4>(g, o, st);
     else launch_tile<Epi, 4, 4>(g, o, st);
   }
@@ -253,6 +266,8 @@ int stride_tc_set_stream_config(int32_t index) {
 }
 
 int stride_tc_stream_config_count(void) { return kNumDecodeCfgs; }
+
+int stride_tc_last_stream_config(void) { return g_last_cfg; }
 
 int stride_tc_stream_config(int32_t index, int32_t* out6) {
   if (index < 0 || index >= kNumDecodeCfgs || !out6) return fail(STRIDE_TC_EINVAL, "decode config index out of range");
