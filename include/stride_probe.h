@@ -18,6 +18,14 @@ extern "C" {
 int stride_probe_mfma_tiles(const uint16_t* a, const uint16_t* b, const float* c, float* out, int32_t tiles,
                             void* stream);
 
+/* Sustained MFMA issue rate: `blocks` workgroups of 4 waves each run `iters`
+ * rounds of 8 independent v_mfma_f32_16x16x32_bf16 from registers (16384 flops
+ * each); time it to get the achievable dense bf16 rate. */
+int stride_probe_mfma_rate(float* out, int32_t blocks, int32_t iters, void* stream);
+/* variant 1: 16 independent 16x16x32 accumulators per round; variant 2: 4
+ * independent v_mfma_f32_32x32x16_bf16 (32768 flops each) per round. */
+int stride_probe_mfma_rate_variant(float* out, int32_t blocks, int32_t iters, int32_t variant, void* stream);
+
 /* Streams `bytes` (a multiple of 16) from `buf` with `blocks` workgroups of 256
  * threads, each thread keeping `unroll` (1, 4, 8 or 16) 16-byte loads in flight,
  * consecutive threads on consecutive 16-byte words; writes one xor-checksum word

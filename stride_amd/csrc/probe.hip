@@ -45,7 +45,82 @@ __global__ __launch_bounds__(256) void k_read(const u32x4* buf, int64_t words, u
   }
 }
 
+// Back-to-back independent MFMAs from registers only: 8 accumulators per wave,
+// `iters` rounds. Measures the sustained v_mfma_f32_16x16x32_bf16 issue rate.
+__global__ __launch_bounds__(256) void k_mfma_rate(float* out, int iters) {
+  const int lane = threadIdx.x & 63;
+  u32x4 a = {static_cast<uint32_t>(lane) * 0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
+  u32x4 b = {0x3f803f80u, static_cast<uint32_t>(lane), 0x3f803f80u, 0x3f803f80u};
+  f32x4 acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = mfma(a, b, acc[i]);
+  }
+  f32x4 s = acc[0];
+#pragma unroll
+  for (int i = 1; i < 8; ++i) s = s + acc[i];
+  if (s[0] == 12345.0f) out[threadIdx.x] = s[1];  // keeps the chain alive
+}
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// Variants for comparison: 16 accumulators of 16x16x32, and 4 of 32x32x16
+// (32768 flops each).
+__global__ __launch_bounds__(256) void k_mfma_rate16(float* out, int iters) {
+  const int lane = threadIdx.x & 63;
+  u32x4 a = {static_cast<uint32_t>(lane) * 0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
+  u32x4 b = {0x3f803f80u, static_cast<uint32_t>(lane), 0x3f803f80u, 0x3f803f80u};
+  f32x4 acc[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[i] = mfma(a, b, acc[i]);
+  }
+  f32x4 s = acc[0];
+#pragma unroll
+  for (int i = 1; i < 16; ++i) s = s + acc[i];
+  if (s[0] == 12345.0f) out[threadIdx.x] = s[1];
+}
+
+__global__ __launch_bounds__(256) void k_mfma_rate32(float* out, int iters) {
+  const int lane = threadIdx.x & 63;
+  u32x4 a = {static_cast<uint32_t>(lane) * 0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
+  u32x4 b = {0x3f803f80u, static_cast<uint32_t>(lane), 0x3f803f80u, 0x3f803f80u};
+  f32x16 acc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) acc[i][j] = 0.f;
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), as_bf16x8(b), acc[i], 0, 0, 0);
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) s += acc[i][0] + acc[i][5];
+  if (s == 12345.0f) out[threadIdx.x] = s;
+}
+
 }  // namespace
+
+extern "C" int stride_probe_mfma_rate_variant(float* out, int32_t blocks, int32_t iters, int32_t variant, void* stream) {
+  if (!out || blocks <= 0 || iters <= 0) return 1;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (variant == 1) hipLaunchKernelGGL(k_mfma_rate16, dim3(blocks), dim3(256), 0, st, out, iters);
+  else if (variant == 2) hipLaunchKernelGGL(k_mfma_rate32, dim3(blocks), dim3(256), 0, st, out, iters);
+  else return 1;
+  return static_cast<int>(hipGetLastError());
+}
+
+extern "C" int stride_probe_mfma_rate(float* out, int32_t blocks, int32_t iters, void* stream) {
+  if (!out || blocks <= 0 || iters <= 0) return 1;
+  hipLaunchKernelGGL(k_mfma_rate, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream), out, iters);
+  return static_cast<int>(hipGetLastError());
+}
 
 extern "C" int stride_probe_mfma_tiles(const uint16_t* a, const uint16_t* b, const float* c, float* out, int32_t tiles,
                                        void* stream) {

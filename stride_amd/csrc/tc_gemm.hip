@@ -35,6 +35,7 @@
 #include <string>
 
 #include "tc_epilogue.hpp"
+#include "tc_pipe.hpp"
 #include "tc_stream.hpp"
 #include "tc_tile.hpp"
 
@@ -196,6 +197,77 @@ int launch_tile(Geometry g, const typename Epi::Out& o, hipStream_t st) {
   return 0;
 }
 
+template <class Epi, int WRT, int WLT, int WM, int WN, int KC, int NS, int OCC>
+void launch_pipe(Geometry g, const typename Epi::Out& o, int smax, hipStream_t st) {
+  constexpr int BR = WM * WRT, BL = WN * WLT;
+  int blocks = 0;
+  for (int i = 0; i < g.nseg; ++i) {
+    g.seg[i].blocks = (g.seg[i].row_tiles + BR - 1) / BR;
+    blocks += g.seg[i].blocks;
+  }
+  blocks *= (g.lane_groups + BL - 1) / BL;
+  if (smax > 1)
+    hipLaunchKernelGGL((k_pipe<Epi, WRT, WLT, WM, WN, KC, NS, OCC, true>), dim3(blocks), dim3(kWave * WM * WN), 0, st, g, o);
+  else
+    hipLaunchKernelGGL((k_pipe<Epi, WRT, WLT, WM, WN, KC, NS, OCC, false>), dim3(blocks), dim3(kWave * WM * WN), 0, st, g, o);
+}
+
+// Prefill configurations of k_pipe: (WRT, WLT, WM, WN, KC, NS, OCC). For the
+// paired gate/up GEMM WRT counts pairs and is halved (two matrices per row tile).
+// Index -3 - i in the tuning hook selects configuration i.
+#define STRIDE_TC_PIPE_CONFIGS(X) \
+  X(0, 4, 4, 2, 2, 2, 3, 1)       \
+  X(1, 4, 4, 4, 2, 2, 2, 1)       \
+  X(2, 4, 4, 2, 4, 2, 2, 1)       \
+  X(3, 8, 4, 2, 4, 2, 2, 1)       \
+  X(4, 4, 8, 4, 2, 2, 2, 1)       \
+  X(5, 4, 8, 2, 2, 2, 3, 1)       \
+  X(6, 4, 4, 4, 4, 2, 2, 1)       \
+  X(7, 8, 4, 2, 2, 2, 3, 1)       \
+  X(8, 4, 4, 4, 2, 2, 3, 1)       \
+  X(9, 4, 8, 2, 2, 2, 2, 1)
+
+constexpr int kNumPipeCfgs = 10;
+int g_forced_pipe = -1;
+
+template <class Epi>
+void launch_pipe_cfg(int idx, const Geometry& g, const typename Epi::Out& o, int smax, hipStream_t st) {
+  switch (idx) {
+#define STRIDE_TC_PIPE_CASE(i, WRT, WLT, WM, WN, KC, NS, OCC)                                              \
+  case i:                                                                                                 \
+    launch_pipe<Epi, (Epi::kMats == 2 ? (WRT > 2 ? WRT / 2 : WRT) : WRT), WLT, WM, WN, KC, NS, OCC>(g, o, smax, st); \
+    break;
+    STRIDE_TC_PIPE_CONFIGS(STRIDE_TC_PIPE_CASE)
+#undef STRIDE_TC_PIPE_CASE
+    default:
+      break;
+  }
+}
+
+// Default prefill configuration (from measured sweeps): 256-row x 256-lane tiles
+// (8 waves of 4x8) when there are no K splits to carry and enough row tiles;
+// 256 x 128 (8 waves of 4x4, splits folded in registers) when the grid still
+// fills the CUs; 128 x 128 (4 waves) for small matrices.
+int pick_pipe(const Geometry& g, int smax) {
+  int rows = 0;
+  for (int i = 0; i < g.nseg; ++i) rows += g.seg[i].row_tiles;
+  if (smax == 1 && rows >= 512) return 4;
+  const int blocks_256x128 = ((rows + 15) / 16) * ((g.lane_groups + 7) / 8);
+  return blocks_256x128 >= 256 ? 8 : 0;
+}
+
+bool pipe_cfg_fits(int idx, const Geometry& g) {
+  static const int kc[] = {
+#define STRIDE_TC_PIPE_KC(i, WRT, WLT, WM, WN, KC, NS, OCC) KC,
+      STRIDE_TC_PIPE_CONFIGS(STRIDE_TC_PIPE_KC)
+#undef STRIDE_TC_PIPE_KC
+  };
+  const int chunks = g.col_tiles >> 1;
+  for (int i = 0; i < g.nseg; ++i)
+    if ((chunks / g.seg[i].splits) % kc[idx] != 0) return false;
+  return true;
+}
+
 // Largest lane-tile count served by the streaming kernel.
 constexpr int kStreamMaxLaneTiles = 8;
 
@@ -218,9 +290,17 @@ int run(Geometry g, const typename Epi::Out& o, hipStream_t st) {
     g_last_cfg = idx;
     launch_decode_cfg<Epi>(idx, g, o, st);
   } else {
-    g_last_cfg = -2;
-    if constexpr (Epi::kMats == 2) launch_tile<Epi, 2, 4>(g, o, st);
-    else launch_tile<Epi, 4, 4>(g, o, st);
+    int pidx = pick_pipe(g, smax);
+    if (g_forced_pipe >= 0) pidx = g_forced_pipe;
+    if (!pipe_cfg_fits(pidx, g)) pidx = 0;
+    if (pipe_cfg_fits(pidx, g)) {
+      g_last_cfg = -3 - pidx;
+      launch_pipe_cfg<Epi>(pidx, g, o, smax, st);
+    } else {
+      g_last_cfg = -2;
+      if constexpr (Epi::kMats == 2) launch_tile<Epi, 2, 4>(g, o, st);
+      else launch_tile<Epi, 4, 4>(g, o, st);
+    }
   }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(static_cast<int>(e), std::string("kernel launch failed: ") + hipGetErrorString(e));
@@ -260,8 +340,13 @@ static_assert(sizeof(StrideTcLmFullParams) == 48, "TcLmFullParams layout");
 extern "C" {
 
 int stride_tc_set_stream_config(int32_t index) {
-  if (index < -1 || index >= kNumDecodeCfgs) return fail(STRIDE_TC_EINVAL, "decode config index out of range");
+  if (index <= -3 && -3 - index < kNumPipeCfgs) {
+    g_forced_pipe = -3 - index;
+    return 0;
+  }
+  if (index < -1 || index >= kNumDecodeCfgs) return fail(STRIDE_TC_EINVAL, "config index out of range");
   g_forced_cfg = index;
+  if (index == -1) g_forced_pipe = -1;
   return 0;
 }
 

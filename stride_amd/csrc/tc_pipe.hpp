@@ -1,0 +1,205 @@
+// Prefill-regime kernel: a multi-stage LDS pipeline fed by direct global->LDS
+// loads (global_load_lds_dwordx4, gfx950).
+//
+// A workgroup of WM x WN wavefronts owns a block of BR = WM*WRT row tiles by
+// BL = WN*WLT lane tiles. K is consumed in stages of KC 32-column chunks. For
+// each stage the workgroup copies M*BR weight chunks and BL activation chunks
+// (1 KiB each) from HBM straight into an NS-deep LDS ring: one wave instruction
+// moves one chunk, each lane fetching the 16 bytes its MFMA fragment position
+// needs, so the chunk lands in LDS already in fragment order and every later
+// ds_read_b128 is a linear, conflict-free 1 KiB read. No registers hold data in
+// flight, so up to NS stages (tens of KiB) are outstanding per workgroup.
+//
+// Synchronisation per stage: each wave waits until its own copies of the stage
+// have landed (s_waitcnt vmcnt with the later stages still outstanding), then one
+// s_barrier makes every wave's copies visible and guarantees that the slot about
+// to be refilled has been consumed. The raw s_barrier is used instead of
+// __syncthreads() because the latter also waits for every outstanding load.
+//
+// Arithmetic: per output tile, the chunks of each split are chained in ascending
+// order by v_mfma_f32_16x16x32_bf16 into an accumulator that starts at zero (at h
+// for split 0 of a residual GEMM) and finished splits are folded into a running
+// sum, y = ((c0 + c1) + c2) + ..., exactly as the decode kernels compute it.
+#pragma once
+
+#include "tc_epilogue.hpp"
+
+namespace stride_tc {
+
+#define STRIDE_TC_GLOBAL(p) ((const __attribute__((address_space(1))) void*)(p))
+#define STRIDE_TC_LDS(p) ((__attribute__((address_space(3))) void*)(p))
+
+// s_waitcnt immediate for "at most n vector-memory operations outstanding"
+// (gfx9 encoding: vmcnt low bits [3:0], high bits [15:14]; expcnt and lgkmcnt
+// left at their no-wait maxima).
+constexpr int vmcnt_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
+// The same with lgkmcnt = 0 (all LDS reads of this wave returned).
+constexpr int vm_lgkm0_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4); }
+
+template <class Epi, int WRT, int WLT, int WM, int WN, int KC, int NS, int OCC, bool HASY>
+__global__ __launch_bounds__(kWave * WM * WN, OCC) void k_pipe(Geometry g, typename Epi::Out o) {
+  constexpr int M = Epi::kMats;
+  constexpr int NW = WM * WN;
+  constexpr int BR = WM * WRT, BL = WN * WLT;
+  constexpr int NBLK = (M * BR + BL) * KC;          // 1 KiB chunks per stage
+  static_assert(NBLK % NW == 0, "stage copies must split evenly over the waves");
+  constexpr int PER_WAVE = NBLK / NW;               // copy instructions per wave per stage
+  constexpr int STAGE = NBLK * kWave;               // u32x4 slots per stage
+  __shared__ u32x4 ring[NS * STAGE];
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int wr = wave / WN, wn = wave % WN;
+  const int lblocks = (g.lane_groups + BL - 1) / BL;
+
+  // Block -> (segment, row block, lane block): groups of G row blocks walk the
+  // lane blocks together so that consecutive workgroups (which the hardware puts
+  // on one XCD after xcd_remap) share activation tiles in L2.
+  int b = xcd_remap(blockIdx.x, gridDim.x);
+  int si = 0;
+  while (si + 1 < g.nseg && b >= g.seg[si].blocks * lblocks) {
+    b -= g.seg[si].blocks * lblocks;
+    ++si;
+  }
+  const Segment& sg = g.seg[si];
+  constexpr int G = 8;
+  const int group = b / (G * lblocks);
+  const int gsize = min(G, sg.blocks - group * G);
+  const int within = b % (G * lblocks);
+  const int rb = group * G + within % gsize;
+  const int lb = within / gsize;
+  const int rt0 = rb * BR, lt0 = lb * BL;
+
+  const int chunks = g.col_tiles >> 1;
+  const int per = chunks / sg.splits;
+  const int nst = chunks / KC;
+  const int64_t strip = static_cast<int64_t>(g.col_tiles) * kTileElems;
+  const int foff = frag_offset(lane);
+
+  // This wave's copy sources: block j = wave + i*NW of each stage.
+  const char* src[PER_WAVE];
+#pragma unroll
+  for (int i = 0; i < PER_WAVE; ++i) {
+    const int j = wave + i * NW;
+    const int kc = j % KC, blk = j / KC;
+    const uint16_t* base;
+    if (blk < M * BR) {
+      const int m = blk / BR;
+      const int rt = min(rt0 + blk % BR, sg.row_tiles - 1);
+      base = sg.w[m] + rt * strip;
+    } else {
+      const int lt = min(lt0 + blk - M * BR, g.lane_groups - 1);
+      base = g.x + lt * strip;
+    }
+    src[i] = reinterpret_cast<const char*>(base) + static_cast<int64_t>(kc) * kChunkBytes + foff;
+  }
+  auto issue = [&](int stage) {
+    u32x4* dst = ring + (stage % NS) * STAGE;
+#pragma unroll
+    for (int i = 0; i < PER_WAVE; ++i) {
+      const int j = wave + i * NW;
+      __builtin_amdgcn_global_load_lds(STRIDE_TC_GLOBAL(src[i] + static_cast<int64_t>(stage) * KC * kChunkBytes),
+                                       STRIDE_TC_LDS(dst + j * kWave), 16, 0, 0);
+    }
+  };
+
+  static_assert(KC % 2 == 0, "fragment double buffering assumes an even chunk count per stage");
+  f32x4 acc[M][WRT][WLT];
+  f32x4 y[HASY ? M : 1][HASY ? WRT : 1][HASY ? WLT : 1];
+  u32x4 fa[2][M][WRT], fb[2][WLT];  // fragments of the current and the next chunk
+
+  auto read_frags = [&](int buf, int stage, int kc) {
+    const u32x4* stg = ring + (stage % NS) * STAGE;
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+      for (int r = 0; r < WRT; ++r) fa[buf][m][r] = stg[((m * BR + wr * WRT + r) * KC + kc) * kWave + lane];
+#pragma unroll
+    for (int l = 0; l < WLT; ++l) fb[buf][l] = stg[((M * BR + wn * WLT + l) * KC + kc) * kWave + lane];
+  };
+  // Wait until stage `next` has landed everywhere (later stages may stay in
+  // flight) and this wave's LDS reads have returned, then barrier.
+  auto sync_for = [&](int next) {
+    const int ahead = min(NS - 2, nst - 1 - next);
+    if (ahead >= NS - 2) __builtin_amdgcn_s_waitcnt(vm_lgkm0_imm((NS - 2) * PER_WAVE));
+    else if (ahead == 2) __builtin_amdgcn_s_waitcnt(vm_lgkm0_imm(2 * PER_WAVE));
+    else if (ahead == 1) __builtin_amdgcn_s_waitcnt(vm_lgkm0_imm(PER_WAVE));
+    else __builtin_amdgcn_s_waitcnt(vm_lgkm0_imm(0));
+    __builtin_amdgcn_s_barrier();
+  };
+
+#pragma unroll
+  for (int st = 0; st < NS; ++st)
+    if (st < nst) issue(st);
+  sync_for(0);
+  read_frags(0, 0, 0);
+
+  // One stage: KC chunks; the fragments of chunk kc+1 are read while chunk kc's
+  // MFMAs run. Before the last chunk, the wave waits for stage i+1, hands stage
+  // i's slot back to the copy engine and starts reading stage i+1.
+  auto stage = [&](int i) {
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc) {
+      const int cur = kc & 1, nxt = cur ^ 1;
+      if (kc + 1 < KC) {
+        read_frags(nxt, i, kc + 1);
+      } else if (i + 1 < nst) {
+        sync_for(i + 1);
+        if (i + NS < nst) issue(i + NS);
+        read_frags(nxt, i + 1, 0);
+      }
+#pragma unroll
+      for (int l = 0; l < WLT; ++l)
+#pragma unroll
+        for (int m = 0; m < M; ++m)
+#pragma unroll
+          for (int r = 0; r < WRT; ++r) acc[m][r][l] = mfma(fa[cur][m][r], fb[cur][l], acc[m][r][l]);
+    }
+  };
+
+  const int stages_per_split = per / KC;
+  int i = 0;
+  for (int s = 0; s < sg.splits; ++s) {
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+      for (int r = 0; r < WRT; ++r)
+#pragma unroll
+        for (int l = 0; l < WLT; ++l) {
+          acc[m][r][l] = f32x4{0.f, 0.f, 0.f, 0.f};
+          if constexpr (Epi::kInitFromOutput) {
+            const int rt = rt0 + wr * WRT + r, lt = lt0 + wn * WLT + l;
+            if (s == 0 && rt < sg.row_tiles && lt < g.lane_groups) acc[m][r][l] = Epi::init(o, rt, lt, lane);
+          }
+        }
+    for (int j = 0; j < stages_per_split; ++j, ++i) stage(i);
+    if constexpr (HASY) {
+#pragma unroll
+      for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int r = 0; r < WRT; ++r)
+#pragma unroll
+          for (int l = 0; l < WLT; ++l) y[m][r][l] = s == 0 ? acc[m][r][l] : y[m][r][l] + acc[m][r][l];
+    }
+  }
+
+#pragma unroll
+  for (int r = 0; r < WRT; ++r) {
+    const int rt = rt0 + wr * WRT + r;
+    if (rt >= sg.row_tiles) continue;
+#pragma unroll
+    for (int l = 0; l < WLT; ++l) {
+      const int lt = lt0 + wn * WLT + l;
+      if (lt >= g.lane_groups) continue;
+      f32x4 t[M];
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        if constexpr (HASY) t[m] = y[m][r][l];
+        else t[m] = acc[m][r][l];
+      }
+      Epi::apply(o, g, si, rt, lt, t, lane);
+    }
+  }
+}
+
+}  // namespace stride_tc

@@ -21,6 +21,10 @@ def load():
         lib.stride_probe_mfma_tiles.restype = C.c_int
         lib.stride_probe_read.argtypes = [vp, C.c_int64, vp, C.c_int32, C.c_int32, vp]
         lib.stride_probe_read.restype = C.c_int
+        lib.stride_probe_mfma_rate.argtypes = [vp, C.c_int32, C.c_int32, vp]
+        lib.stride_probe_mfma_rate.restype = C.c_int
+        lib.stride_probe_mfma_rate_variant.argtypes = [vp, C.c_int32, C.c_int32, C.c_int32, vp]
+        lib.stride_probe_mfma_rate_variant.restype = C.c_int
         _lib = lib
     return _lib
 
@@ -36,3 +40,15 @@ def read(buf, out, blocks: int, unroll: int, stream: int) -> None:
                                   stream)
     if rc:
         raise RuntimeError(f"stride_probe_read failed ({rc})")
+
+
+def mfma_rate(out, blocks: int, iters: int, stream: int) -> None:
+    rc = load().stride_probe_mfma_rate(out.data_ptr(), blocks, iters, stream)
+    if rc:
+        raise RuntimeError(f"stride_probe_mfma_rate failed ({rc})")
+
+
+def mfma_rate_variant(out, blocks: int, iters: int, variant: int, stream: int) -> None:
+    rc = load().stride_probe_mfma_rate_variant(out.data_ptr(), blocks, iters, variant, stream)
+    if rc:
+        raise RuntimeError(f"stride_probe_mfma_rate_variant failed ({rc})")

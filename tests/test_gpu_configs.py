@@ -71,3 +71,23 @@ def test_all_configs_identical(setup, m):
                 assert got[k] == ref[k], f"config {i} {cfgs[i]} changes {k} bits at M={m}"
     finally:
         _lib.set_stream_config(-1)
+
+
+@pytest.mark.parametrize("m", [150, 290, 1024])
+def test_all_prefill_configs_identical(setup, m):
+    """The same for the prefill (LDS-pipelined) kernel configurations; their
+    outputs must also match the decode kernels row for row."""
+    W, x, h = setup
+    xx = {k: torch.cat([v] * 9)[:m] for k, v in x.items()}
+    hh = torch.cat([h] * 9)[:m]
+    _lib.set_stream_config(-1)
+    ref = run_all(W, xx, hh, m)
+    try:
+        for i in range(10):
+            say("prefill config", i, "M =", m)
+            _lib.set_stream_config(-3 - i)
+            got = run_all(W, xx, hh, m)
+            for k in ref:
+                assert got[k] == ref[k], f"prefill config {i} changes {k} bits at M={m}"
+    finally:
+        _lib.set_stream_config(-1)
