@@ -98,6 +98,7 @@ class Buffers:
         self.slots = torch.arange(m, dtype=torch.int32, device=dev)
         self.pos = torch.full((m,), 10, dtype=torch.int32, device=dev)
         self.best = harness.best_init(m, dev)
+        self.best0 = harness.best_init(m, dev)
 
 
 def step_ops(model, b):
@@ -112,7 +113,9 @@ def step_ops(model, b):
         ops.append(("o", lambda L=L: harness.gemm_residual(L["o"], b.attn, b.h, m)))
         ops.append(("gate_up", lambda L=L: harness.mlp13(L["w1"], L["w3"], b.x, m, out=b.z)))
         ops.append(("down", lambda L=L: harness.gemm_residual(L["w2"], b.z, b.h, m)))
-    ops.append(("lm_head", lambda: harness.lm_greedy(model.lm, b.x, m, VOCAB, best=b.best)))
+    # best is re-initialised before every argmax, as the engine uploads {-inf, -1}
+    # each step (reference src/engine.cpp:423-424); the reset is part of the op.
+    ops.append(("lm_head", lambda: (b.best.copy_(b.best0), harness.lm_greedy(model.lm, b.x, m, VOCAB, best=b.best))))
     return ops
 
 
@@ -253,8 +256,7 @@ def main():
 
     from stride_amd import harness
 
-    best0 = harness.best_init(a.m, dev)
-    step = [lambda: b.best.copy_(best0)] + [f for _, f in ops]
+    step = [f for _, f in ops]
 
     # Eager (host-launched) rate, for reference.
     for _ in range(a.warmup):

@@ -54,6 +54,7 @@ __device__ __forceinline__ int locate_segment(const Geometry& g, int& rb) {
 
 struct EpiResidual {  // h <- h + W x   (reference src/kernels_tc.cu:438-501)
   static constexpr int kMats = 1;
+  static constexpr bool kReduce = false;
   static constexpr bool kInitFromOutput = true;
   struct Out {
     float* h;
@@ -72,6 +73,7 @@ struct EpiResidual {  // h <- h + W x   (reference src/kernels_tc.cu:438-501)
 
 struct EpiLogits {  // logits tiles [rt][lt][16 rows][16 lanes]  (src/kernels_tc.cu:632-655)
   static constexpr int kMats = 1;
+  static constexpr bool kReduce = false;
   static constexpr bool kInitFromOutput = false;
   struct Out {
     float* logits;
@@ -88,6 +90,7 @@ struct EpiLogits {  // logits tiles [rt][lt][16 rows][16 lanes]  (src/kernels_tc
 
 struct EpiGateUp {  // z = bf16(det_silu(W1 x) * (W3 x))  (src/kernels_tc.cu:505-564)
   static constexpr int kMats = 2;
+  static constexpr bool kReduce = false;
   static constexpr bool kInitFromOutput = false;
   struct Out {
     uint16_t* z;
@@ -107,43 +110,105 @@ struct EpiGateUp {  // z = bf16(det_silu(W1 x) * (W3 x))  (src/kernels_tc.cu:505
   }
 };
 
+// Lexicographic merge of argmax candidates (larger value, then smaller index;
+// index -1 = none). Associative and commutative, so any merge order gives the
+// same result.
+__device__ __forceinline__ void arg_merge(float& bv, int32_t& bi, float ov, int32_t oi) {
+  if (oi >= 0 && (bi < 0 || better_than(ov, oi, bv, bi))) {
+    bv = ov;
+    bi = oi;
+  }
+}
+
 struct EpiArgmax {  // per-lane greedy argmax  (src/kernels_tc.cu:590-630)
   static constexpr int kMats = 1;
   static constexpr bool kInitFromOutput = false;
+  // Kernels reduce the candidates of all row tiles a workgroup owns before they
+  // touch `best`, so each lane sees one compare-and-swap per workgroup instead
+  // of one per row tile (thousands of racing updates otherwise serialise).
+  static constexpr bool kReduce = true;
   struct Out {
     StrideBestEntry* best;
     int32_t vocab;
+    // When set, a workgroup stores its per-lane candidate to cand[row block *
+    // rows + lane] instead of updating `best`; k_argmax_finish then reduces the
+    // row blocks of each lane and merges once into `best`.
+    unsigned long long* cand;
   };
   __device__ static f32x4 init(const Out&, int, int, int) { return f32x4{0.f, 0.f, 0.f, 0.f}; }
-  __device__ static void apply(const Out& o, const Geometry& g, int, int rt, int lt, const f32x4* y, int lane) {
-    float bv = f32_of(0xFF800000u);
-    int32_t bi = -1;
+  // Merge tile (rt, *) into this lane column's candidate (bv, bi); after the call
+  // every lane l holds the candidate of batch lane l % 16. Whole-wave call.
+  __device__ static void merge_tile(const Out& o, int rt, const f32x4& y, int lane, float& bv, int32_t& bi) {
+    float tv = f32_of(0xFF800000u);
+    int32_t ti = -1;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int index = rt * 16 + (lane >> 4) * 4 + i;
-      if (index < o.vocab && y[0][i] > bv) {
-        bv = y[0][i];
-        bi = index;
+      if (index < o.vocab && y[i] > tv) {  // ascending rows, strict '>' (ties keep the smaller index)
+        tv = y[i];
+        ti = index;
       }
     }
-    // Merge the four row groups of this lane column; the merge is the
-    // lexicographic max, so the exchange order does not matter.
 #pragma unroll
     for (int sh = 16; sh <= 32; sh <<= 1) {
-      const float ov = __shfl_xor(bv, sh);
-      const int32_t oi = __shfl_xor(bi, sh);
-      if (oi >= 0 && (bi < 0 || better_than(ov, oi, bv, bi))) {
-        bv = ov;
-        bi = oi;
-      }
+      const float ov = __shfl_xor(tv, sh);
+      const int32_t oi = __shfl_xor(ti, sh);
+      arg_merge(tv, ti, ov, oi);
     }
+    arg_merge(bv, bi, tv, ti);
+  }
+  __device__ static void commit(const Out& o, const Geometry& g, int lt, int lane, float bv, int32_t bi, int rb) {
+    const int j = lt * 16 + (lane & 15);
+    if (lane >= 16 || j >= g.rows) return;
+    if (o.cand) {
+      o.cand[static_cast<int64_t>(rb) * g.rows + j] =
+          (static_cast<unsigned long long>(static_cast<uint32_t>(bi)) << 32) | u32_of(bv);
+    } else if (bi >= 0) {
+      best_update(&o.best[j], bv, bi);
+    }
+  }
+  __device__ static void apply(const Out& o, const Geometry& g, int, int rt, int lt, const f32x4* y, int lane) {
+    float bv = f32_of(0xFF800000u);
+    int32_t bi = -1;
+    merge_tile(o, rt, y[0], lane, bv, bi);
     const int j = lt * 16 + (lane & 15);
     if (lane < 16 && j < g.rows && bi >= 0) best_update(&o.best[j], bv, bi);
   }
 };
 
+// Second pass of the greedy LM head: lane j reduces the candidates of all nrb
+// row blocks (any order gives the same lexicographic max) and merges the winner
+// into best[j] (the caller's initial entry takes part, as in the reference).
+__global__ __launch_bounds__(256) void k_argmax_finish(const unsigned long long* __restrict__ cand, int nrb, int rows,
+                                                       StrideBestEntry* best) {
+  const int j = blockIdx.x;
+  float bv = f32_of(0xFF800000u);
+  int32_t bi = -1;
+  for (int rb = threadIdx.x; rb < nrb; rb += 256) {
+    const unsigned long long c = cand[static_cast<int64_t>(rb) * rows + j];
+    arg_merge(bv, bi, f32_of(static_cast<uint32_t>(c)), static_cast<int32_t>(c >> 32));
+  }
+  __shared__ float sv[256];
+  __shared__ int32_t si[256];
+  sv[threadIdx.x] = bv;
+  si[threadIdx.x] = bi;
+  __syncthreads();
+  for (int h = 128; h > 0; h >>= 1) {
+    if (threadIdx.x < h) {
+      float v = sv[threadIdx.x];
+      int32_t i = si[threadIdx.x];
+      arg_merge(v, i, sv[threadIdx.x + h], si[threadIdx.x + h]);
+      sv[threadIdx.x] = v;
+      si[threadIdx.x] = i;
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0 && si[0] >= 0) best_update(&best[j], sv[0], si[0]);
+}
+
 struct EpiQkv {  // RoPE + q store + bf16 KV append  (src/kernels_tc.cu:347-432)
   static constexpr int kMats = 1;
+  static constexpr bool kReduce = false;
   static constexpr bool kInitFromOutput = false;
   struct Out {
     float* q_out;

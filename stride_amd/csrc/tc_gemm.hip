@@ -135,6 +135,26 @@ constexpr DecodeCfg kDecodeCfgs[] = {STRIDE_TC_DECODE_CONFIGS(STRIDE_TC_ROW)};
 constexpr int kNumDecodeCfgs = sizeof(kDecodeCfgs) / sizeof(kDecodeCfgs[0]);
 
 int g_forced_cfg = -1;
+
+// Argmax candidate scratch for the greedy LM head: one 8-byte (value, index)
+// slot per (row block, batch lane). A fixed file-scope device array, so the
+// entry point allocates nothing; launches on one device share it and must be
+// ordered on one stream (the reference keeps every launch on one stream,
+// src/kernels.cu:457-460).
+constexpr int64_t kCandSlots = int64_t{1} << 21;  // 16 MiB
+__device__ __align__(256) unsigned long long g_cand[kCandSlots];
+
+unsigned long long* cand_scratch() {
+  static unsigned long long* cache[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  if (!cache[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_cand)) != hipSuccess) return nullptr;
+    cache[dev] = static_cast<unsigned long long*>(p);
+  }
+  return cache[dev];
+}
 int g_last_cfg = -1;  // configuration of the last decode-regime launch (-2: prefill kernel)
 
 template <class Epi, int R, int LT, int WS, int WR, int U, bool XL>
@@ -271,36 +291,72 @@ bool pipe_cfg_fits(int idx, const Geometry& g) {
 // Largest lane-tile count served by the streaming kernel.
 constexpr int kStreamMaxLaneTiles = 8;
 
+// Row tiles per workgroup of prefill configuration idx.
+int pipe_rows_per_block(int idx, int mats) {
+  static const int wrt[] = {
+#define STRIDE_TC_PIPE_WRT(i, WRT, WLT, WM, WN, KC, NS, OCC) WRT,
+      STRIDE_TC_PIPE_CONFIGS(STRIDE_TC_PIPE_WRT)
+#undef STRIDE_TC_PIPE_WRT
+  };
+  static const int wm[] = {
+#define STRIDE_TC_PIPE_WM(i, WRT, WLT, WM, WN, KC, NS, OCC) WM,
+      STRIDE_TC_PIPE_CONFIGS(STRIDE_TC_PIPE_WM)
+#undef STRIDE_TC_PIPE_WM
+  };
+  const int r = mats == 2 && wrt[idx] > 2 ? wrt[idx] / 2 : wrt[idx];  // as launch_pipe_cfg halves it
+  return wm[idx] * r;
+}
+
 template <class Epi>
-int run(Geometry g, const typename Epi::Out& o, hipStream_t st) {
+int run(Geometry g, const typename Epi::Out& o_in, hipStream_t st) {
   if (g.rows == 0) return 0;
+  typename Epi::Out o = o_in;
   int smax = 1;
   for (int i = 0; i < g.nseg; ++i) {
     if (g.seg[i].splits > 16) return fail(STRIDE_TC_EINVAL, "split count above 16");
     smax = g.seg[i].splits > smax ? g.seg[i].splits : smax;
   }
   const int T = g.lane_groups;
+  int kind = 0, idx = 0, rows_per_block = 0;  // kind 0: decode, 1: pipe, 2: legacy tile
   if (T <= kStreamMaxLaneTiles) {
-    int idx = pick_decode(T, smax, Epi::kMats, g.nseg);
+    idx = pick_decode(T, smax, Epi::kMats, g.nseg);
     if (g_forced_cfg >= 0 && decode_cfg_fits(kDecodeCfgs[g_forced_cfg], g, smax, Epi::kMats)) idx = g_forced_cfg;
     if (!decode_cfg_fits(kDecodeCfgs[idx], g, smax, Epi::kMats)) {
       // fall back to a register-only in-workgroup configuration with a wave per split
       idx = smax == 1 ? 3 : (smax == 2 ? 2 : (smax <= 8 ? 0 : 18));
     }
+    rows_per_block = kDecodeCfgs[idx].wr * kDecodeCfgs[idx].r;
+  } else {
+    kind = 1;
+    idx = pick_pipe(g, smax);
+    if (g_forced_pipe >= 0) idx = g_forced_pipe;
+    if (!pipe_cfg_fits(idx, g)) idx = 0;
+    if (!pipe_cfg_fits(idx, g)) kind = 2;
+    else rows_per_block = pipe_rows_per_block(idx, Epi::kMats);
+  }
+  // Greedy LM head: two passes through the candidate scratch when it fits.
+  int nrb = 0;
+  if constexpr (Epi::kReduce) {
+    o.cand = nullptr;
+    if (kind != 2 && g.nseg == 1) {
+      nrb = (g.seg[0].row_tiles + rows_per_block - 1) / rows_per_block;
+      if (static_cast<int64_t>(nrb) * g.rows <= kCandSlots) o.cand = cand_scratch();
+      if (!o.cand) nrb = 0;
+    }
+  }
+  if (kind == 0) {
     g_last_cfg = idx;
     launch_decode_cfg<Epi>(idx, g, o, st);
+  } else if (kind == 1) {
+    g_last_cfg = -3 - idx;
+    launch_pipe_cfg<Epi>(idx, g, o, smax, st);
   } else {
-    int pidx = pick_pipe(g, smax);
-    if (g_forced_pipe >= 0) pidx = g_forced_pipe;
-    if (!pipe_cfg_fits(pidx, g)) pidx = 0;
-    if (pipe_cfg_fits(pidx, g)) {
-      g_last_cfg = -3 - pidx;
-      launch_pipe_cfg<Epi>(pidx, g, o, smax, st);
-    } else {
-      g_last_cfg = -2;
-      if constexpr (Epi::kMats == 2) launch_tile<Epi, 2, 4>(g, o, st);
-      else launch_tile<Epi, 4, 4>(g, o, st);
-    }
+    g_last_cfg = -2;
+    if constexpr (Epi::kMats == 2) launch_tile<Epi, 2, 4>(g, o, st);
+    else launch_tile<Epi, 4, 4>(g, o, st);
+  }
+  if constexpr (Epi::kReduce) {
+    if (nrb > 0) hipLaunchKernelGGL(k_argmax_finish, dim3(g.rows), dim3(256), 0, st, o.cand, nrb, g.rows, o.best);
   }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(static_cast<int>(e), std::string("kernel launch failed: ") + hipGetErrorString(e));
@@ -414,7 +470,7 @@ int stride_tc_lm_greedy(const StrideTcLmGreedyParams* p, int, int, void* stream)
   if (!p->x || !p->best) return fail(STRIDE_TC_EINVAL, "lm_greedy: null x or best");
   if (p->vocab <= 0 || p->vocab > p->m.groups * 16) return fail(STRIDE_TC_EINVAL, "lm_greedy: vocab must be in (0, groups*16]");
   Geometry g = single(p->l, p->x, p->m, nullptr);
-  EpiArgmax::Out o{p->best, p->vocab};
+  EpiArgmax::Out o{p->best, p->vocab, nullptr};
   return run<EpiArgmax>(g, o, static_cast<hipStream_t>(stream));
 }
 

@@ -183,6 +183,43 @@ __global__ __launch_bounds__(kWave * WM * WN, OCC) void k_pipe(Geometry g, typen
     }
   }
 
+  if constexpr (Epi::kReduce) {
+    // Merge this workgroup's row tiles per batch lane, then one update per lane.
+    __syncthreads();  // the LDS ring is reused for the candidates
+    float* cand_v = reinterpret_cast<float*>(ring);
+    int32_t* cand_i = reinterpret_cast<int32_t*>(ring) + WM * BL * 16;
+#pragma unroll
+    for (int l = 0; l < WLT; ++l) {
+      float bv = f32_of(0xFF800000u);
+      int32_t bi = -1;
+#pragma unroll
+      for (int r = 0; r < WRT; ++r) {
+        const int rt = rt0 + wr * WRT + r;
+        if (rt >= sg.row_tiles) continue;
+        if constexpr (HASY) Epi::merge_tile(o, rt, y[0][r][l], lane, bv, bi);
+        else Epi::merge_tile(o, rt, acc[0][r][l], lane, bv, bi);
+      }
+      if (lane < 16) {
+        cand_v[(wr * BL + wn * WLT + l) * 16 + lane] = bv;
+        cand_i[(wr * BL + wn * WLT + l) * 16 + lane] = bi;
+      }
+    }
+    __syncthreads();
+    if (wr == 0) {
+#pragma unroll
+      for (int l = 0; l < WLT; ++l) {
+        const int lt = lt0 + wn * WLT + l;
+        if (lt >= g.lane_groups) continue;
+        float v = f32_of(0xFF800000u);
+        int32_t i = -1;
+#pragma unroll
+        for (int w = 0; w < WM; ++w)
+          arg_merge(v, i, cand_v[(w * BL + wn * WLT + l) * 16 + (lane & 15)], cand_i[(w * BL + wn * WLT + l) * 16 + (lane & 15)]);
+        Epi::commit(o, g, lt, lane, v, i, rb);
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int r = 0; r < WRT; ++r) {
     const int rt = rt0 + wr * WRT + r;

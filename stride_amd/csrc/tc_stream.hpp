@@ -37,6 +37,10 @@ __global__ __launch_bounds__(kWave * WS * WR) void k_stream(Geometry g, typename
   __shared__ u32x4 smem[kSlots];
   f32x4* ybuf = reinterpret_cast<f32x4*>(smem);
   u32x4* xs = smem;
+  // Per-wave argmax candidates (value, index) for the workgroup-level reduction.
+  constexpr int kCand = Epi::kReduce ? WS * WR * LT * 16 : 1;
+  __shared__ float cand_v[kCand];
+  __shared__ int32_t cand_i[kCand];
 
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
@@ -212,7 +216,63 @@ __global__ __launch_bounds__(kWave * WS * WR) void k_stream(Geometry g, typename
     }
   }
 
-  if constexpr (WS == 1) {
+  if constexpr (Epi::kReduce) {
+    // Candidates of every tile this workgroup owns are merged first; then one
+    // wave publishes a single update per batch lane.
+    float bv[LT];
+    int32_t bi[LT];
+#pragma unroll
+    for (int l = 0; l < LT; ++l) {
+      bv[l] = f32_of(0xFF800000u);
+      bi[l] = -1;
+    }
+    if constexpr (WS == 1) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        if (rt_first + r >= sg.row_tiles) continue;
+#pragma unroll
+        for (int l = 0; l < LT; ++l) Epi::merge_tile(o, rt_first + r, acc[0][r][l], lane, bv[l], bi[l]);
+      }
+    } else {
+      for (int s = 0; s < splits; ++s) {
+        if (ws == s) {
+#pragma unroll
+          for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int l = 0; l < LT; ++l) {
+              f32x4& y = ybuf[((wr * R + r) * LT + l) * kWave + lane];
+              y = s == 0 ? acc[0][r][l] : y + acc[0][r][l];
+            }
+        }
+        __syncthreads();
+      }
+      for (int t = wave; t < WR * R; t += WS * WR) {
+        const int twr = t / R, r = t % R;
+        const int rt = rb * (WR * R) + twr * R + r;
+        if (rt >= sg.row_tiles) continue;
+#pragma unroll
+        for (int l = 0; l < LT; ++l) Epi::merge_tile(o, rt, ybuf[((twr * R + r) * LT + l) * kWave + lane], lane, bv[l], bi[l]);
+      }
+    }
+    if (lane < 16) {
+#pragma unroll
+      for (int l = 0; l < LT; ++l) {
+        cand_v[(wave * LT + l) * 16 + lane] = bv[l];
+        cand_i[(wave * LT + l) * 16 + lane] = bi[l];
+      }
+    }
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+      for (int l = 0; l < LT; ++l) {
+        if (l >= nlt) continue;
+        float v = f32_of(0xFF800000u);
+        int32_t i = -1;
+        for (int w = 0; w < WS * WR; ++w) arg_merge(v, i, cand_v[(w * LT + l) * 16 + (lane & 15)], cand_i[(w * LT + l) * 16 + (lane & 15)]);
+        Epi::commit(o, g, lt0 + l, lane, v, i, rb);
+      }
+    }
+  } else if constexpr (WS == 1) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       if (rt_first + r >= sg.row_tiles) continue;
