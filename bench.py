@@ -181,6 +181,24 @@ def time_ops(torch, ops, reps):
     return res
 
 
+# Epilogue of the kernel serving each op (the name rocprofv3 records).
+OP_EPILOGUE = {"gate_up": "EpiGateUp", "qkv": "EpiQkv", "lm_head": "EpiArgmax"}
+
+
+def measured_traffic(op, m):
+    """HBM bytes per launch of `op` from the committed counter profile of this
+    benchmark (FETCH_SIZE and WRITE_SIZE runs, each scaled by what the counter
+    reads for a plain copy of known size), or None when no profile covers it."""
+    path = os.path.join(ROOT, "profiles", f"decode_gemm_set_m{m}_traffic.json")
+    epi = OP_EPILOGUE.get(op)
+    if not epi or not os.path.exists(path):
+        return None
+    with open(path) as f:
+        prof = json.load(f)
+    hits = [v["hbm_bytes"] for k, v in prof["kernels"].items() if epi in k]
+    return int(hits[0]) if len(hits) == 1 else None
+
+
 def cpu_baseline(seconds, threads):
     """The reference's exact path (oracle/_ref: its src/kernels.cu compiled as C++)
     on this host: one decode step at batch 1, sampled as one layer's four GEMMs
@@ -292,8 +310,8 @@ def main():
     fl, by = work(dom, a.m)
     ach = by / per[dom] / 1e9
     roof = {"kernel": dom, "bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None, "avg_launch_us": round(per[dom] * 1e6, 2),
-            "algorithmic_bytes": int(by)}
+            "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dom, a.m),
+            "avg_launch_us": round(per[dom] * 1e6, 2), "algorithmic_bytes": int(by)}
     weight_bytes = sum(work(n, 0)[1] for n, _ in ops)
 
     table = []

@@ -130,10 +130,11 @@ struct EpiArgmax {  // per-lane greedy argmax  (src/kernels_tc.cu:590-630)
   struct Out {
     StrideBestEntry* best;
     int32_t vocab;
-    // When set, a workgroup stores its per-lane candidate to cand[row block *
-    // rows + lane] instead of updating `best`; k_argmax_finish then reduces the
-    // row blocks of each lane and merges once into `best`.
+    // When set, a workgroup stores its per-lane candidate to cand[lane * nrb +
+    // row block] instead of updating `best`; k_argmax_finish then reduces the
+    // row blocks of each lane (contiguous) and merges once into `best`.
     unsigned long long* cand;
+    int32_t nrb;
   };
   __device__ static f32x4 init(const Out&, int, int, int) { return f32x4{0.f, 0.f, 0.f, 0.f}; }
   // Merge tile (rt, *) into this lane column's candidate (bv, bi); after the call
@@ -161,7 +162,7 @@ struct EpiArgmax {  // per-lane greedy argmax  (src/kernels_tc.cu:590-630)
     const int j = lt * 16 + (lane & 15);
     if (lane >= 16 || j >= g.rows) return;
     if (o.cand) {
-      o.cand[static_cast<int64_t>(rb) * g.rows + j] =
+      o.cand[static_cast<int64_t>(j) * o.nrb + rb] =
           (static_cast<unsigned long long>(static_cast<uint32_t>(bi)) << 32) | u32_of(bv);
     } else if (bi >= 0) {
       best_update(&o.best[j], bv, bi);
@@ -185,7 +186,7 @@ __global__ __launch_bounds__(256) void k_argmax_finish(const unsigned long long*
   float bv = f32_of(0xFF800000u);
   int32_t bi = -1;
   for (int rb = threadIdx.x; rb < nrb; rb += 256) {
-    const unsigned long long c = cand[static_cast<int64_t>(rb) * rows + j];
+    const unsigned long long c = cand[static_cast<int64_t>(j) * nrb + rb];
     arg_merge(bv, bi, f32_of(static_cast<uint32_t>(c)), static_cast<int32_t>(c >> 32));
   }
   __shared__ float sv[256];

@@ -342,6 +342,7 @@ int run(Geometry g, const typename Epi::Out& o_in, hipStream_t st) {
       nrb = (g.seg[0].row_tiles + rows_per_block - 1) / rows_per_block;
       if (static_cast<int64_t>(nrb) * g.rows <= kCandSlots) o.cand = cand_scratch();
       if (!o.cand) nrb = 0;
+      o.nrb = nrb;
     }
   }
   if (kind == 0) {
@@ -470,7 +471,7 @@ int stride_tc_lm_greedy(const StrideTcLmGreedyParams* p, int, int, void* stream)
   if (!p->x || !p->best) return fail(STRIDE_TC_EINVAL, "lm_greedy: null x or best");
   if (p->vocab <= 0 || p->vocab > p->m.groups * 16) return fail(STRIDE_TC_EINVAL, "lm_greedy: vocab must be in (0, groups*16]");
   Geometry g = single(p->l, p->x, p->m, nullptr);
-  EpiArgmax::Out o{p->best, p->vocab, nullptr};
+  EpiArgmax::Out o{p->best, p->vocab, nullptr, 0};
   return run<EpiArgmax>(g, o, static_cast<hipStream_t>(stream));
 }
 

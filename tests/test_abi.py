@@ -93,3 +93,23 @@ def test_rejects_bad_arguments_without_launch():
     # rows == 0 is a no-op, as the reference's launch<> with zero blocks
     z = tc.TcGemmResidualParams(tc.Lanes(0, 0, 0, 0), 0x1000, tc.GemmMat(0x2000, 4, 64), 0x3000)
     assert lib.stride_tc_gemm_residual(C.byref(z), 1, 1, None) == 0
+
+
+def test_cpp_shim_compiles_against_reference_header(tmp_path):
+    """include/stride_tc_shim.hpp defines stride::tc_* with the reference
+    signatures over the C ABI; its static_asserts check the engine's PODs against
+    the ABI structs. Compiled here against the reference's own kernels_tc.h."""
+    if not os.path.exists(os.path.join(REF_SRC, "kernels_tc.h")):
+        pytest.skip("reference tree absent")
+    tu = tmp_path / "tc_gemm_hip.cpp"
+    tu.write_text('#include "kernels_tc.h"\n#include "stride_tc_shim.hpp"\n'
+                  'namespace stride { void* tc_stream() { return nullptr; } }\n')
+    subprocess.run(["g++", "-std=c++17", "-Wall", "-Werror", "-c", f"-I{REF_SRC}", f"-I{os.path.join(ROOT, 'include')}",
+                    str(tu), "-o", str(tmp_path / "tu.o")], check=True)
+    syms = subprocess.run(["nm", "-C", str(tmp_path / "tu.o")], capture_output=True, text=True, check=True).stdout
+    for name in ("stride::tc_qkv(stride::TcQkvParams const&)",
+                 "stride::tc_gemm_residual(stride::TcGemmResidualParams const&, int, int)",
+                 "stride::tc_mlp13(stride::TcMlp13Params const&, int, int)",
+                 "stride::tc_lm_greedy(stride::TcLmGreedyParams const&, int, int)",
+                 "stride::tc_lm_full(stride::TcLmFullParams const&, int)"):
+        assert name in syms, name
