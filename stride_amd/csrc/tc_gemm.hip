@@ -122,7 +122,14 @@ bool mat_ok(const StrideGemmMat& m, const char* name, std::string& why) {
   S(32, 1, 8, 8, 2, 1, true)          \
   S(33, 2, 2, 8, 1, 4, false)         \
   S(34, 1, 1, 8, 2, 8, false)         \
-  S(35, 2, 1, 8, 1, 8, false)
+  S(35, 2, 1, 8, 1, 8, false)         \
+  S(36, 1, 4, 2, 4, 8, true)          \
+  S(37, 1, 8, 2, 4, 8, true)          \
+  S(38, 2, 4, 2, 4, 8, true)          \
+  S(39, 1, 8, 1, 8, 4, true)          \
+  S(40, 2, 8, 1, 8, 4, true)          \
+  S(41, 1, 4, 2, 8, 8, true)          \
+  S(42, 2, 8, 2, 4, 4, true)
 
 struct DecodeCfg {
   int r, lt, ws, wr, u;
@@ -184,7 +191,11 @@ void launch_decode_cfg(int idx, const Geometry& g, const typename Epi::Out& o, h
 
 // Can configuration c serve this launch?
 bool decode_cfg_fits(const DecodeCfg& c, Geometry g, int smax, int mats) {
-  const int u = c.u / mats > 0 ? c.u / mats : 1;
+  int u = c.u / mats > 0 ? c.u / mats : 1;
+  if (c.xl) {
+    const int umax = 128 / (c.ws * 2 * c.lt) > 0 ? 128 / (c.ws * 2 * c.lt) : 1;
+    u = u < umax ? u : umax;  // as k_stream clamps it
+  }
   if (c.ws < smax) return false;
   if (c.xl && (u * c.lt) % c.wr == 0) {
     const int chunks = g.col_tiles >> 1;
@@ -202,7 +213,7 @@ int pick_decode(int T, int smax, int mats, int nseg) {
   if (T <= 1) return smax == 1 ? 4 : (smax == 2 ? 1 : 0);
   if (T <= 2) return smax == 1 ? 7 : (smax == 2 ? 22 : 1);
   if (T <= 4) return smax == 1 ? 13 : (smax == 2 ? 27 : (nseg == 3 ? 33 : 5));
-  return smax == 1 ? 16 : (smax == 2 ? 10 : (nseg == 3 ? 9 : 33));
+  return smax == 1 ? 16 : (smax == 2 ? 36 : (nseg == 3 ? 9 : 33));
 }
 
 template <class Epi, int WRT, int WLT>

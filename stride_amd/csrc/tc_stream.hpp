@@ -24,7 +24,11 @@ template <class Epi, int R, int LT, int WS, int WR, int UC, bool XLC>
 __global__ __launch_bounds__(kWave * WS * WR) void k_stream(Geometry g, typename Epi::Out o) {
   constexpr int M = Epi::kMats;
   // UC counts weight chunks in flight per batch; a paired GEMM loads M chunks per step.
-  constexpr int U = UC / M > 0 ? UC / M : 1;
+  constexpr int U0 = UC / M > 0 ? UC / M : 1;
+  // With x staged in LDS, keep the ring (WS groups x 2 buffers x U chunks x LT
+  // tiles x 1 KiB) within 128 KiB.
+  constexpr int UMAX = XLC ? (128 / (WS * 2 * LT) > 0 ? 128 / (WS * 2 * LT) : 1) : U0;
+  constexpr int U = U0 < UMAX ? U0 : UMAX;
   // x staging needs each batch to split evenly over the row waves of a split group.
   constexpr bool XL = XLC && (U * LT) % WR == 0;
   constexpr int kY = WS > 1 ? WR * M * R * LT * kWave : 1;           // combine buffer (f32x4 slots)
@@ -104,8 +108,12 @@ __global__ __launch_bounds__(kWave * WS * WR) void k_stream(Geometry g, typename
 
   // Chunk range of this wave's split (idle waves of a WG with fewer splits run an
   // empty range but still take part in the barriers).
-  const int c0 = active ? ws * per : 0;
-  const int c1 = active ? c0 + per : 0;
+  // The bounds are made wave-uniform (scalar registers): control flow around
+  // MFMAs must be scalar branches, because an MFMA ignores the EXEC mask and
+  // would still accumulate inside an exec-masked block the compiler chose not
+  // to branch around.
+  const int c0 = __builtin_amdgcn_readfirstlane(active ? ws * per : 0);
+  const int c1 = __builtin_amdgcn_readfirstlane(active ? c0 + per : 0);
   const int nbatch = (c1 - c0) / U;
   const int cb = c0 + nbatch * U;  // batched range [c0, cb), then single chunks up to c1
 

@@ -1,0 +1,95 @@
+"""Machine-code checks on this repository's own gfx950 build (CPU only).
+
+An MFMA ignores the EXEC mask: if one sits in a block that the compiler
+entered by narrowing EXEC and chose not to branch around (it skips
+`s_cbranch_execz` for short blocks on the assumption that masked lanes do
+nothing), the MFMA accumulates even when no lane is meant to. That silently
+adds a chunk twice. Every k-loop must therefore guard MFMAs with scalar
+(wave-uniform) branches only; this test disassembles the built library and
+fails if any MFMA is reachable, in straight-line order, after an EXEC
+narrowing with no `s_cbranch_execz` in between.
+"""
+import os
+import struct
+import subprocess
+import tempfile
+
+import pytest
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(os.path.dirname(HERE), "stride_amd")
+OBJDUMP = "/opt/rocm/llvm/bin/llvm-objdump"
+MAGIC = b"__CLANG_OFFLOAD_BUNDLE__"
+
+
+def code_object(lib_path: str) -> bytes:
+    """The gfx950 code object from the offload bundle embedded in a hipcc-built .so
+    (bundle layout: magic, u64 count, then per entry u64 offset, u64 size, u64
+    triple length, triple)."""
+    data = open(lib_path, "rb").read()
+    base = data.find(MAGIC)
+    assert base >= 0, "no offload bundle in " + lib_path
+    (count,) = struct.unpack_from("<Q", data, base + len(MAGIC))
+    p = base + len(MAGIC) + 8
+    for _ in range(count):
+        off, size, tlen = struct.unpack_from("<QQQ", data, p)
+        p += 24
+        triple = data[p:p + tlen].decode()
+        p += tlen
+        if "gfx950" in triple:
+            return data[base + off:base + off + size]
+    raise AssertionError("no gfx950 code object in " + lib_path)
+
+
+NARROW = ("s_and_saveexec", "s_andn2_saveexec", "s_or_saveexec", "s_xor_saveexec", "s_and_b64 exec",
+          "s_andn2_b64 exec", "s_xor_b64 exec")
+RESTORE = ("s_or_b64 exec", "s_mov_b64 exec", "s_cbranch_execz", "s_cbranch_execnz")
+
+
+def masked_mfmas(disasm: str):
+    """(function, instruction) pairs where an MFMA follows an EXEC narrowing
+    with no branch-around or restore in between."""
+    out, fn, masked = [], None, False
+    for line in disasm.splitlines():
+        s = line.strip()
+        if s.endswith(">:"):
+            fn, masked = s[s.find("<") + 1:-2], False
+            continue
+        ins = s.split("//")[0].strip()
+        if not ins:
+            continue
+        if ins.startswith(NARROW):
+            masked = True
+        elif ins.startswith(RESTORE):
+            masked = False
+        elif ins.startswith("v_mfma") and masked:
+            out.append((fn, ins))
+    return out
+
+
+def test_scanner_flags_unguarded_mfma():
+    bad = """
+<k>:
+	s_and_saveexec_b64 s[2:3], s[0:1]
+	v_mfma_f32_16x16x32_bf16 v[6:9], v[10:13], v[26:29], v[6:9]
+	s_or_b64 exec, exec, s[2:3]
+"""
+    good = bad.replace("s_and_saveexec_b64 s[2:3], s[0:1]",
+                       "s_and_saveexec_b64 s[2:3], s[0:1]\n\ts_cbranch_execz .LBB0_2")
+    assert masked_mfmas(bad) and not masked_mfmas(good)
+
+
+@pytest.mark.parametrize("lib", ["libstride_tc.so", "libstride_probe.so"])
+def test_no_mfma_under_exec_mask(lib):
+    path = os.path.join(PKG, lib)
+    if not os.path.exists(path):
+        pytest.skip(lib + " not built")
+    if not os.path.exists(OBJDUMP):
+        pytest.skip("llvm-objdump not available")
+    with tempfile.TemporaryDirectory() as d:
+        co = os.path.join(d, "k.co")
+        open(co, "wb").write(code_object(path))
+        dis = subprocess.run([OBJDUMP, "-d", "--mcpu=gfx950", co], capture_output=True, text=True, check=True).stdout
+    assert "v_mfma" in dis
+    bad = masked_mfmas(dis)
+    assert not bad, f"{len(bad)} MFMAs under an exec mask, first in {bad[0][0]}"
