@@ -154,9 +154,10 @@ int stride_tc_lm_full(const StrideTcLmFullParams* p, int lane_tiles_per_block, v
  * of n rows and k columns. Depends on (n, k) only. */
 int stride_tc_split_count(int32_t n, int32_t k);
 
-/* Tuning hook, no reference counterpart: force the decode-regime (M <= 128)
- * kernel configuration `index` (0 .. stride_tc_stream_config_count()-1) for the
- * calling process, or -1 for the automatic choice. Every configuration computes
+/* Tuning hook, no reference counterpart: force the register-streaming kernel
+ * configuration `index` (0 .. stride_tc_stream_config_count()-1) for launches of
+ * at most 8 lane tiles, or the LDS-pipelined configuration -3-i for every launch
+ * it can serve, or -1 for the automatic choice. Every configuration computes
  * identical bits; this only changes speed. A configuration that cannot serve a
  * launch is ignored for it. */
 int stride_tc_set_stream_config(int32_t index);
@@ -164,7 +165,9 @@ int stride_tc_stream_config_count(void);
 /* Configuration used by the last launch in this process (-2: the prefill
  * kernel, -1: none yet). */
 int stride_tc_last_stream_config(void);
-/* Writes (R, LT, WS, WR, U, XL) of configuration `index` into out6. */
+/* Writes (R, LT, WS, WR, U, flags) of configuration `index` into out6; flags bit 0:
+ * activations staged in LDS, bit 1: one K split per workgroup (the last workgroup
+ * of each tile group to finish combines the partials). */
 int stride_tc_stream_config(int32_t index, int32_t* out6);
 
 /* Message for the last nonzero return on this thread ("" if none). */

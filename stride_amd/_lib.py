@@ -165,7 +165,8 @@ def split_count(n: int, k: int) -> int:
 
 
 def stream_configs():
-    """[(R, LT, WS, WR, U, XL)] of the decode-regime kernel configurations."""
+    """[(R, LT, WS, WR, U, flags)] of the decode-regime kernel configurations
+    (flags bit 0: x staged in LDS, bit 1: one split per workgroup)."""
     lib = load()
     out = []
     for i in range(lib.stride_tc_stream_config_count()):

@@ -16,9 +16,27 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "../../include/stride_tc.h"
 
 namespace stride_tc {
+
+// Compile-time loop: calls f(std::integral_constant<int, i>) for i = 0 .. N-1.
+// Used where register arrays must be indexed with constants and `#pragma unroll`
+// may give up on a large body (a partially rolled loop would index the array at
+// run time and move it to scratch memory).
+template <int I, int N, class F>
+__device__ __forceinline__ void unroll_impl(F& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    unroll_impl<I + 1, N>(f);
+  }
+}
+template <int N, class F>
+__device__ __forceinline__ void unroll(F f) {
+  unroll_impl<0, N>(f);
+}
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));

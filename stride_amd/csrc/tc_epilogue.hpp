@@ -27,6 +27,13 @@ struct Geometry {
   int32_t lane_groups;
   int32_t nseg;
   Segment seg[3];
+  // Cross-workgroup split partials (k_stream with XS): fp32 fragments indexed
+  // ((tile * part_splits + split) * mats + m) * 64 + lane, tile = segment tile
+  // base + rt * lane_groups + lt, and one arrival counter per (row block, lane
+  // group) unit, zero between launches. Unused (null) otherwise.
+  float* part;
+  int32_t* split_cnt;
+  int32_t part_splits;
 };
 
 // Spread consecutive logical blocks over one XCD: hardware hands workgroup i to
@@ -38,11 +45,23 @@ __device__ __forceinline__ int xcd_remap(int i, int n) {
   return (i & 7) * (full >> 3) + (i >> 3);
 }
 
-__device__ __forceinline__ int locate_segment(const Geometry& g, int& rb) {
+// Segment i of g with i known only at run time. Selecting among the three by
+// value keeps the kernel argument in registers (indexing the argument array with
+// a run-time index makes the compiler copy it to scratch memory).
+__device__ __forceinline__ Segment seg_at(const Geometry& g, int i) {
+  return i == 0 ? g.seg[0] : (i == 1 ? g.seg[1] : g.seg[2]);
+}
+
+// Segment of logical row block rb (made segment-relative), with `per` logical
+// blocks per row block of a segment's count.
+__device__ __forceinline__ int locate_segment(const Geometry& g, int& rb, int per = 1) {
   int s = 0;
-  while (s + 1 < g.nseg && rb >= g.seg[s].blocks) {
-    rb -= g.seg[s].blocks;
-    ++s;
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    if (s == k && k + 1 < g.nseg && rb >= g.seg[k].blocks * per) {
+      rb -= g.seg[k].blocks * per;
+      s = k + 1;
+    }
   }
   return s;
 }
@@ -60,13 +79,13 @@ struct EpiResidual {  // h <- h + W x   (reference src/kernels_tc.cu:438-501)
     float* h;
     int32_t h_tiles;
   };
-  __device__ static float* at(const Out& o, int rt, int lt, int lane) {
+  __device__ __forceinline__ static float* at(const Out& o, int rt, int lt, int lane) {
     return o.h + (static_cast<int64_t>(lt) * o.h_tiles + rt) * kTileElems + (lane & 15) * 16 + (lane >> 4) * 4;
   }
-  __device__ static f32x4 init(const Out& o, int rt, int lt, int lane) {
+  __device__ __forceinline__ static f32x4 init(const Out& o, int rt, int lt, int lane) {
     return *reinterpret_cast<const f32x4*>(at(o, rt, lt, lane));
   }
-  __device__ static void apply(const Out& o, const Geometry&, int, int rt, int lt, const f32x4* y, int lane) {
+  __device__ __forceinline__ static void apply(const Out& o, const Geometry&, int, int rt, int lt, const f32x4* y, int lane) {
     *reinterpret_cast<f32x4*>(at(o, rt, lt, lane)) = y[0];
   }
 };
@@ -78,8 +97,8 @@ struct EpiLogits {  // logits tiles [rt][lt][16 rows][16 lanes]  (src/kernels_tc
   struct Out {
     float* logits;
   };
-  __device__ static f32x4 init(const Out&, int, int, int) { return f32x4{0.f, 0.f, 0.f, 0.f}; }
-  __device__ static void apply(const Out& o, const Geometry& g, int, int rt, int lt, const f32x4* y, int lane) {
+  __device__ __forceinline__ static f32x4 init(const Out&, int, int, int) { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+  __device__ __forceinline__ static void apply(const Out& o, const Geometry& g, int, int rt, int lt, const f32x4* y, int lane) {
     float* base = o.logits + (static_cast<int64_t>(rt) * g.lane_groups + lt) * kTileElems + (lane >> 4) * 64 + (lane & 15);
     base[0] = y[0][0];
     base[16] = y[0][1];
@@ -96,8 +115,8 @@ struct EpiGateUp {  // z = bf16(det_silu(W1 x) * (W3 x))  (src/kernels_tc.cu:505
     uint16_t* z;
     int32_t z_tiles;
   };
-  __device__ static f32x4 init(const Out&, int, int, int) { return f32x4{0.f, 0.f, 0.f, 0.f}; }
-  __device__ static void apply(const Out& o, const Geometry&, int, int rt, int lt, const f32x4* y, int lane) {
+  __device__ __forceinline__ static f32x4 init(const Out&, int, int, int) { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+  __device__ __forceinline__ static void apply(const Out& o, const Geometry&, int, int rt, int lt, const f32x4* y, int lane) {
     uint32_t b[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -136,10 +155,10 @@ struct EpiArgmax {  // per-lane greedy argmax  (src/kernels_tc.cu:590-630)
     unsigned long long* cand;
     int32_t nrb;
   };
-  __device__ static f32x4 init(const Out&, int, int, int) { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+  __device__ __forceinline__ static f32x4 init(const Out&, int, int, int) { return f32x4{0.f, 0.f, 0.f, 0.f}; }
   // Merge tile (rt, *) into this lane column's candidate (bv, bi); after the call
   // every lane l holds the candidate of batch lane l % 16. Whole-wave call.
-  __device__ static void merge_tile(const Out& o, int rt, const f32x4& y, int lane, float& bv, int32_t& bi) {
+  __device__ __forceinline__ static void merge_tile(const Out& o, int rt, const f32x4& y, int lane, float& bv, int32_t& bi) {
     float tv = f32_of(0xFF800000u);
     int32_t ti = -1;
 #pragma unroll
@@ -158,7 +177,7 @@ struct EpiArgmax {  // per-lane greedy argmax  (src/kernels_tc.cu:590-630)
     }
     arg_merge(bv, bi, tv, ti);
   }
-  __device__ static void commit(const Out& o, const Geometry& g, int lt, int lane, float bv, int32_t bi, int rb) {
+  __device__ __forceinline__ static void commit(const Out& o, const Geometry& g, int lt, int lane, float bv, int32_t bi, int rb) {
     const int j = lt * 16 + (lane & 15);
     if (lane >= 16 || j >= g.rows) return;
     if (o.cand) {
@@ -168,7 +187,7 @@ struct EpiArgmax {  // per-lane greedy argmax  (src/kernels_tc.cu:590-630)
       best_update(&o.best[j], bv, bi);
     }
   }
-  __device__ static void apply(const Out& o, const Geometry& g, int, int rt, int lt, const f32x4* y, int lane) {
+  __device__ __forceinline__ static void apply(const Out& o, const Geometry& g, int, int rt, int lt, const f32x4* y, int lane) {
     float bv = f32_of(0xFF800000u);
     int32_t bi = -1;
     merge_tile(o, rt, y[0], lane, bv, bi);
@@ -222,15 +241,15 @@ struct EpiQkv {  // RoPE + q store + bf16 KV append  (src/kernels_tc.cu:347-432)
     const int32_t* row_slot;
     const int32_t* row_pos;
   };
-  __device__ static f32x4 init(const Out&, int, int, int) { return f32x4{0.f, 0.f, 0.f, 0.f}; }
-  __device__ static uint16_t* kv_row(const Out& o, int which, int head, int slot, int pos) {
+  __device__ __forceinline__ static f32x4 init(const Out&, int, int, int) { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+  __device__ __forceinline__ static uint16_t* kv_row(const Out& o, int which, int head, int slot, int pos) {
     const StrideKvRef& kv = o.kv;
     const int64_t block = kv.table[static_cast<int64_t>(slot) * kv.max_blocks + (pos >> o.page_shift)];
     const int token = pos & ((1 << o.page_shift) - 1);
     return static_cast<uint16_t*>(kv.arena) + block * kv.block_elems + o.layer * kv.layer_elems + which * kv.which_elems +
            head * kv.group_elems + static_cast<int64_t>(token) * kv.head_dim;
   }
-  __device__ static void apply(const Out& o, const Geometry& g, int kind, int rt, int lt, const f32x4* y, int lane) {
+  __device__ __forceinline__ static void apply(const Out& o, const Geometry& g, int kind, int rt, int lt, const f32x4* y, int lane) {
     // Row m (< 8) of the tile pairs with row m + 8: lanes l and l ^ 32.
     float partner[4];
 #pragma unroll
@@ -245,29 +264,55 @@ struct EpiQkv {  // RoPE + q store + bf16 KV append  (src/kernels_tc.cu:347-432)
     if (j >= g.rows) return;
     const int pos = o.row_pos[j];
     const int slot = o.row_slot[j];
+    // This lane holds dims d..d+3 (rows 4*(lane/16)+i of the tile) and, from
+    // its partner, d+half..d+half+3: each half is written as one vector when
+    // the destination is aligned for it.
+    const int d = d0 + (lane >> 4) * 4;
+    float lo[4], hi[4];
+    if (kind == 2) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int d = d0 + (lane >> 4) * 4 + i;
-      const float a = y[0][i];
-      const float b = partner[i];
-      if (kind == 2) {
-        uint16_t* dst = kv_row(o, 1, head, slot, pos);
-        dst[d] = static_cast<uint16_t>(bf16_rne(a));
-        dst[d + half] = static_cast<uint16_t>(bf16_rne(b));
+      for (int i = 0; i < 4; ++i) {
+        lo[i] = y[0][i];
+        hi[i] = partner[i];
+      }
+    } else {
+      const float* cs = o.rope + (static_cast<int64_t>(pos) * half + d) * 2;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float co = cs[2 * i], si = cs[2 * i + 1];
+        const float a = y[0][i], b = partner[i];
+        lo[i] = a * co - b * si;
+        hi[i] = b * co + a * si;
+      }
+    }
+    if (kind == 0) {
+      float* q = o.q_out + static_cast<int64_t>(j) * o.q_stride + static_cast<int64_t>(head) * D + d;
+      if ((reinterpret_cast<uintptr_t>(q) & 15) == 0 && (half & 3) == 0) {
+        *reinterpret_cast<f32x4*>(q) = f32x4{lo[0], lo[1], lo[2], lo[3]};
+        *reinterpret_cast<f32x4*>(q + half) = f32x4{hi[0], hi[1], hi[2], hi[3]};
       } else {
-        const float* cs = o.rope + (static_cast<int64_t>(pos) * half + d) * 2;
-        const float co = cs[0], si = cs[1];
-        const float ra = a * co - b * si;
-        const float rb = b * co + a * si;
-        if (kind == 0) {
-          float* q = o.q_out + static_cast<int64_t>(j) * o.q_stride + static_cast<int64_t>(head) * D;
-          q[d] = ra;
-          q[d + half] = rb;
-        } else {
-          uint16_t* dst = kv_row(o, 0, head, slot, pos);
-          dst[d] = static_cast<uint16_t>(bf16_rne(ra));
-          dst[d + half] = static_cast<uint16_t>(bf16_rne(rb));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          q[i] = lo[i];
+          q[half + i] = hi[i];
         }
+      }
+    } else {
+      uint16_t* dst = kv_row(o, kind == 2 ? 1 : 0, head, slot, pos) + d;
+      const uint32_t b0 = bf16_rne(lo[0]), b1 = bf16_rne(lo[1]), b2 = bf16_rne(lo[2]), b3 = bf16_rne(lo[3]);
+      const uint32_t c0 = bf16_rne(hi[0]), c1 = bf16_rne(hi[1]), c2 = bf16_rne(hi[2]), c3 = bf16_rne(hi[3]);
+      if ((reinterpret_cast<uintptr_t>(dst) & 7) == 0 && (half & 3) == 0) {
+        *reinterpret_cast<u32x2*>(dst) = u32x2{b0 | (b1 << 16), b2 | (b3 << 16)};
+        *reinterpret_cast<u32x2*>(dst + half) = u32x2{c0 | (c1 << 16), c2 | (c3 << 16)};
+      } else {
+        dst[0] = static_cast<uint16_t>(b0);
+        dst[1] = static_cast<uint16_t>(b1);
+        dst[2] = static_cast<uint16_t>(b2);
+        dst[3] = static_cast<uint16_t>(b3);
+        dst[half] = static_cast<uint16_t>(c0);
+        dst[half + 1] = static_cast<uint16_t>(c1);
+        dst[half + 2] = static_cast<uint16_t>(c2);
+        dst[half + 3] = static_cast<uint16_t>(c3);
       }
     }
   }

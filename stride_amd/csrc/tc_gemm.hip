@@ -82,105 +82,145 @@ bool mat_ok(const StrideGemmMat& m, const char* name, std::string& why) {
 }
 
 // Decode-regime configurations of k_stream: (R row tiles per wave, LT lane tiles,
-// WS split waves, WR row waves, U chunks per batch, XL x staged in LDS). Which
+// WS split waves, WR row waves, U chunks per batch, XL x staged in LDS, XS one
+// split per workgroup, the last arriving workgroup of a tile group combining). Which
 // one runs never changes results: all evaluate the same chunk order and the same
 // split combine. The table is indexed by stride_tc_set_stream_config() for tuning
 // sweeps and by pick_decode() otherwise.
 #define STRIDE_TC_DECODE_CONFIGS(S) \
-  S(0, 1, 1, 8, 1, 8, false)          \
-  S(1, 1, 1, 8, 1, 4, false)          \
-  S(2, 1, 1, 2, 4, 8, false)          \
-  S(3, 1, 1, 1, 8, 8, false)          \
-  S(4, 1, 1, 1, 4, 8, false)          \
-  S(5, 1, 2, 8, 1, 8, false)          \
-  S(6, 1, 2, 2, 4, 8, false)          \
-  S(7, 1, 2, 1, 8, 8, false)          \
-  S(8, 1, 4, 8, 1, 4, false)          \
-  S(9, 2, 4, 8, 1, 2, false)          \
-  S(10, 1, 4, 2, 4, 4, false)         \
-  S(11, 1, 4, 2, 4, 2, true)          \
-  S(12, 1, 4, 1, 8, 4, false)         \
-  S(13, 2, 4, 1, 8, 2, true)          \
-  S(14, 1, 8, 8, 1, 2, false)         \
-  S(15, 2, 8, 8, 1, 2, false)         \
-  S(16, 1, 8, 1, 8, 2, true)          \
-  S(17, 1, 8, 1, 8, 2, false)         \
-  S(18, 1, 1, 16, 1, 4, false)        \
-  S(19, 1, 1, 16, 1, 8, false)        \
-  S(20, 1, 2, 16, 1, 4, false)        \
-  S(21, 1, 4, 16, 1, 2, false)        \
-  S(22, 1, 2, 4, 2, 4, false)         \
-  S(23, 1, 1, 4, 2, 8, false)         \
-  S(24, 1, 4, 4, 2, 4, false)         \
-  S(25, 1, 2, 16, 1, 2, false)        \
-  S(26, 1, 1, 16, 1, 2, false)        \
-  S(27, 2, 4, 8, 1, 4, false)         \
-  S(28, 2, 8, 8, 1, 1, false)         \
-  S(29, 4, 4, 8, 1, 1, false)         \
-  S(30, 4, 8, 8, 1, 1, false)         \
-  S(31, 2, 8, 8, 2, 1, true)          \
-  S(32, 1, 8, 8, 2, 1, true)          \
-  S(33, 2, 2, 8, 1, 4, false)         \
-  S(34, 1, 1, 8, 2, 8, false)         \
-  S(35, 2, 1, 8, 1, 8, false)         \
-  S(36, 1, 4, 2, 4, 8, true)          \
-  S(37, 1, 8, 2, 4, 8, true)          \
-  S(38, 2, 4, 2, 4, 8, true)          \
-  S(39, 1, 8, 1, 8, 4, true)          \
-  S(40, 2, 8, 1, 8, 4, true)          \
-  S(41, 1, 4, 2, 8, 8, true)          \
-  S(42, 2, 8, 2, 4, 4, true)
+  S(0, 1, 1, 8, 1, 8, false, false) \
+  S(1, 1, 1, 8, 1, 4, false, false) \
+  S(2, 1, 1, 2, 4, 8, false, false) \
+  S(3, 1, 1, 1, 8, 8, false, false) \
+  S(4, 1, 1, 1, 4, 8, false, false) \
+  S(5, 1, 2, 8, 1, 8, false, false) \
+  S(6, 1, 2, 2, 4, 8, false, false) \
+  S(7, 1, 2, 1, 8, 8, false, false) \
+  S(8, 1, 4, 8, 1, 4, false, false) \
+  S(9, 2, 4, 8, 1, 2, false, false) \
+  S(10, 1, 4, 2, 4, 4, false, false) \
+  S(11, 1, 4, 2, 4, 2, true, false) \
+  S(12, 1, 4, 1, 8, 4, false, false) \
+  S(13, 2, 4, 1, 8, 2, true, false) \
+  S(14, 1, 8, 8, 1, 2, false, false) \
+  S(15, 2, 8, 8, 1, 2, false, false) \
+  S(16, 1, 8, 1, 8, 2, true, false) \
+  S(17, 1, 8, 1, 8, 2, false, false) \
+  S(18, 1, 1, 16, 1, 4, false, false) \
+  S(19, 1, 1, 16, 1, 8, false, false) \
+  S(20, 1, 2, 16, 1, 4, false, false) \
+  S(21, 1, 4, 16, 1, 2, false, false) \
+  S(22, 1, 2, 4, 2, 4, false, false) \
+  S(23, 1, 1, 4, 2, 8, false, false) \
+  S(24, 1, 4, 4, 2, 4, false, false) \
+  S(25, 1, 2, 16, 1, 2, false, false) \
+  S(26, 1, 1, 16, 1, 2, false, false) \
+  S(27, 2, 4, 8, 1, 4, false, false) \
+  S(28, 2, 8, 8, 1, 1, false, false) \
+  S(29, 4, 4, 8, 1, 1, false, false) \
+  S(30, 4, 8, 8, 1, 1, false, false) \
+  S(31, 2, 8, 8, 2, 1, true, false) \
+  S(32, 1, 8, 8, 2, 1, true, false) \
+  S(33, 2, 2, 8, 1, 4, false, false) \
+  S(34, 1, 1, 8, 2, 8, false, false) \
+  S(35, 2, 1, 8, 1, 8, false, false) \
+  S(36, 1, 4, 2, 4, 8, true, false) \
+  S(37, 1, 8, 2, 4, 8, true, false) \
+  S(38, 2, 4, 2, 4, 8, true, false) \
+  S(39, 1, 8, 1, 8, 4, true, false) \
+  S(40, 2, 8, 1, 8, 4, true, false) \
+  S(41, 1, 4, 2, 8, 8, true, false) \
+  S(42, 2, 8, 2, 4, 4, true, false) \
+  S(43, 1, 8, 1, 4, 8, true, true) \
+  S(44, 2, 8, 1, 4, 4, true, true) \
+  S(45, 1, 8, 1, 8, 8, true, true) \
+  S(46, 1, 8, 1, 2, 4, true, true) \
+  S(47, 1, 4, 1, 4, 8, true, true) \
+  S(48, 2, 4, 1, 4, 4, true, true) \
+  S(49, 1, 8, 1, 4, 4, true, true) \
+  S(50, 2, 8, 1, 2, 4, true, true) \
+  S(51, 4, 8, 1, 2, 2, true, true) \
+  S(52, 2, 8, 1, 4, 2, true, true) \
+  S(53, 1, 1, 1, 4, 8, false, true) \
+  S(54, 1, 1, 1, 8, 8, false, true) \
+  S(55, 1, 1, 1, 2, 8, false, true) \
+  S(56, 2, 1, 1, 4, 4, false, true) \
+  S(57, 1, 2, 1, 4, 8, false, true) \
+  S(58, 1, 8, 1, 4, 8, false, true)
 
 struct DecodeCfg {
   int r, lt, ws, wr, u;
-  bool xl;
+  bool xl, xs;
 };
 
-#define STRIDE_TC_ROW(i, R, LT, WS, WR, U, XL) {R, LT, WS, WR, U, XL},
+#define STRIDE_TC_ROW(i, R, LT, WS, WR, U, XL, XS) {R, LT, WS, WR, U, XL, XS},
 constexpr DecodeCfg kDecodeCfgs[] = {STRIDE_TC_DECODE_CONFIGS(STRIDE_TC_ROW)};
 #undef STRIDE_TC_ROW
 constexpr int kNumDecodeCfgs = sizeof(kDecodeCfgs) / sizeof(kDecodeCfgs[0]);
 
 int g_forced_cfg = -1;
 
-// Argmax candidate scratch for the greedy LM head: one 8-byte (value, index)
-// slot per (row block, batch lane). A fixed file-scope device array, so the
-// entry point allocates nothing; launches on one device share it and must be
-// ordered on one stream (the reference keeps every launch on one stream,
-// src/kernels.cu:457-460).
-constexpr int64_t kCandSlots = int64_t{1} << 21;  // 16 MiB
-__device__ __align__(256) unsigned long long g_cand[kCandSlots];
+// Device scratch shared by two uses: the greedy LM head's argmax candidates
+// (one 8-byte (value, index) slot per (row block, batch lane)) and the fp32
+// split partials of cross-workgroup split launches. A fixed file-scope device
+// array, so the entry points allocate nothing; launches on one device share it
+// and must be ordered on one stream (the reference keeps every launch on one
+// stream, src/kernels.cu:457-460).
+constexpr int64_t kScratchBytes = int64_t{16} << 20;
+constexpr int64_t kCandSlots = kScratchBytes / 8;
+__device__ __align__(256) unsigned long long g_scratch[kScratchBytes / 8];
 
-unsigned long long* cand_scratch() {
+// Arrival counters of cross-workgroup split launches, one per (row block, lane
+// group) unit; each launch leaves them at zero.
+constexpr int kSplitUnits = 1 << 16;
+__device__ __align__(256) int32_t g_split_cnt[kSplitUnits];
+
+int32_t* split_counters() {
+  static int32_t* cache[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  if (!cache[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_split_cnt)) != hipSuccess) return nullptr;
+    cache[dev] = static_cast<int32_t*>(p);
+  }
+  return cache[dev];
+}
+
+unsigned long long* scratch_base() {
   static unsigned long long* cache[64] = {};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
   if (!cache[dev]) {
     void* p = nullptr;
-    if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_cand)) != hipSuccess) return nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_scratch)) != hipSuccess) return nullptr;
     cache[dev] = static_cast<unsigned long long*>(p);
   }
   return cache[dev];
 }
 int g_last_cfg = -1;  // configuration of the last decode-regime launch (-2: prefill kernel)
 
-template <class Epi, int R, int LT, int WS, int WR, int U, bool XL>
+template <class Epi, int R, int LT, int WS, int WR, int U, bool XL, bool XS>
 void launch_stream(Geometry g, const typename Epi::Out& o, hipStream_t st) {
-  int blocks = 0;
-  for (int i = 0; i < g.nseg; ++i) {
-    g.seg[i].blocks = (g.seg[i].row_tiles + WR * R - 1) / (WR * R);
-    blocks += g.seg[i].blocks;
+  if constexpr (XS && Epi::kReduce) {
+    return;  // never selected (decode_cfg_fits)
+  } else {
+    int blocks = 0;
+    for (int i = 0; i < g.nseg; ++i) {
+      g.seg[i].blocks = (g.seg[i].row_tiles + WR * R - 1) / (WR * R);
+      blocks += XS ? g.seg[i].blocks * g.seg[i].splits : g.seg[i].blocks;
+    }
+    blocks *= (g.lane_groups + LT - 1) / LT;
+    hipLaunchKernelGGL((k_stream<Epi, R, LT, WS, WR, U, XL, XS>), dim3(blocks), dim3(kWave * WS * WR), 0, st, g, o);
   }
-  blocks *= (g.lane_groups + LT - 1) / LT;
-  hipLaunchKernelGGL((k_stream<Epi, R, LT, WS, WR, U, XL>), dim3(blocks), dim3(kWave * WS * WR), 0, st, g, o);
 }
 
 template <class Epi>
 void launch_decode_cfg(int idx, const Geometry& g, const typename Epi::Out& o, hipStream_t st) {
   switch (idx) {
-#define STRIDE_TC_CASE(i, R, LT, WS, WR, U, XL) \
-  case i:                                       \
-    launch_stream<Epi, R, LT, WS, WR, U, XL>(g, o, st); \
+#define STRIDE_TC_CASE(i, R, LT, WS, WR, U, XL, XS)          \
+  case i:                                                    \
+    launch_stream<Epi, R, LT, WS, WR, U, XL, XS>(g, o, st); \
     break;
     STRIDE_TC_DECODE_CONFIGS(STRIDE_TC_CASE)
 #undef STRIDE_TC_CASE
@@ -189,31 +229,63 @@ void launch_decode_cfg(int idx, const Geometry& g, const typename Epi::Out& o, h
   }
 }
 
+// Output tiles of a launch (all segments).
+int64_t total_tiles(const Geometry& g) {
+  int64_t t = 0;
+  for (int i = 0; i < g.nseg; ++i) t += static_cast<int64_t>(g.seg[i].row_tiles) * g.lane_groups;
+  return t;
+}
+
 // Can configuration c serve this launch?
-bool decode_cfg_fits(const DecodeCfg& c, Geometry g, int smax, int mats) {
+bool decode_cfg_fits(const DecodeCfg& c, Geometry g, int smax, int mats, bool reduce) {
   int u = c.u / mats > 0 ? c.u / mats : 1;
   if (c.xl) {
     const int umax = 128 / (c.ws * 2 * c.lt) > 0 ? 128 / (c.ws * 2 * c.lt) : 1;
     u = u < umax ? u : umax;  // as k_stream clamps it
   }
+  const int chunks = g.col_tiles >> 1;
+  if (c.xs) {
+    if (reduce || c.ws != 1 || smax < 2 || smax > kMaxXSplits) return false;
+    if (total_tiles(g) * smax * mats * 1024 > kScratchBytes) return false;
+    int64_t units = 0;
+    for (int i = 0; i < g.nseg; ++i) units += (g.seg[i].row_tiles + c.wr * c.r - 1) / (c.wr * c.r);
+    if (units * ((g.lane_groups + c.lt - 1) / c.lt) > kSplitUnits) return false;
+    if (c.xl && (u * c.lt) % c.wr == 0)
+      for (int i = 0; i < g.nseg; ++i)
+        if ((chunks / g.seg[i].splits) % u != 0) return false;
+    return true;
+  }
   if (c.ws < smax) return false;
   if (c.xl && (u * c.lt) % c.wr == 0) {
-    const int chunks = g.col_tiles >> 1;
     for (int i = 0; i < g.nseg; ++i)
       if (g.seg[i].splits != c.ws || (chunks / g.seg[i].splits) % u != 0) return false;
   }
   return true;
 }
 
-// Default choice by lane-tile count, split count and segment count, from
-// measured sweeps on MI355X (HIP-graph timing, weights rotated past the MALL).
-int pick_decode(int T, int smax, int mats, int nseg) {
+// Default choice by lane-tile count, split count, segment count and split
+// length, from measured sweeps on MI355X (HIP-graph timing, weights rotated past
+// the MALL).
+int pick_decode(int T, int smax, int mats, int nseg, int per) {
   (void)mats;
   if (smax > 8) return T <= 1 ? 18 : (T <= 2 ? 20 : 21);
-  if (T <= 1) return smax == 1 ? 4 : (smax == 2 ? 1 : 0);
+  if (T <= 1) {
+    if (smax == 1) return 4;
+    if (smax == 2) return 34;
+    return nseg == 1 && per >= 32 ? 53 : 0;  // long splits: one split per workgroup
+  }
   if (T <= 2) return smax == 1 ? 7 : (smax == 2 ? 22 : 1);
   if (T <= 4) return smax == 1 ? 13 : (smax == 2 ? 27 : (nseg == 3 ? 33 : 5));
   return smax == 1 ? 16 : (smax == 2 ? 36 : (nseg == 3 ? 9 : 33));
+}
+
+// Decode batches for which the LDS-pipelined kernel with small blocks measured
+// faster: the LM head (one split) from two lane tiles up and the paired gate/up
+// GEMM from four. Returns a prefill configuration index or -1.
+int pick_decode_pipe(int T, int smax, int mats) {
+  if (smax == 1 && T >= 2) return T <= 4 ? 14 : 8;
+  if (smax == 2 && mats == 2 && T >= 3) return T <= 4 ? 17 : 15;
+  return -1;
 }
 
 template <class Epi, int WRT, int WLT>
@@ -256,9 +328,17 @@ void launch_pipe(Geometry g, const typename Epi::Out& o, int smax, hipStream_t s
   X(6, 4, 4, 4, 4, 2, 2, 1)       \
   X(7, 8, 4, 2, 2, 2, 3, 1)       \
   X(8, 4, 4, 4, 2, 2, 3, 1)       \
-  X(9, 4, 8, 2, 2, 2, 2, 1)
+  X(9, 4, 8, 2, 2, 2, 2, 1)       \
+  X(10, 4, 2, 1, 4, 2, 4, 1)      \
+  X(11, 4, 4, 1, 2, 2, 4, 1)      \
+  X(12, 2, 2, 2, 4, 2, 4, 1)      \
+  X(13, 2, 4, 1, 2, 2, 4, 1)      \
+  X(14, 4, 1, 1, 4, 2, 4, 1)      \
+  X(15, 2, 2, 1, 4, 2, 4, 2)      \
+  X(16, 4, 2, 2, 2, 2, 4, 1)      \
+  X(17, 4, 1, 1, 4, 2, 6, 1)
 
-constexpr int kNumPipeCfgs = 10;
+constexpr int kNumPipeCfgs = 18;
 int g_forced_pipe = -1;
 
 template <class Epi>
@@ -329,10 +409,16 @@ int run(Geometry g, const typename Epi::Out& o_in, hipStream_t st) {
   }
   const int T = g.lane_groups;
   int kind = 0, idx = 0, rows_per_block = 0;  // kind 0: decode, 1: pipe, 2: legacy tile
-  if (T <= kStreamMaxLaneTiles) {
-    idx = pick_decode(T, smax, Epi::kMats, g.nseg);
-    if (g_forced_cfg >= 0 && decode_cfg_fits(kDecodeCfgs[g_forced_cfg], g, smax, Epi::kMats)) idx = g_forced_cfg;
-    if (!decode_cfg_fits(kDecodeCfgs[idx], g, smax, Epi::kMats)) {
+  // A forced prefill configuration (tuning hook) also serves decode batches.
+  const int dpipe = g_forced_cfg >= 0 ? -1 : (g_forced_pipe >= 0 ? g_forced_pipe : pick_decode_pipe(T, smax, Epi::kMats));
+  if (T <= kStreamMaxLaneTiles && dpipe >= 0 && pipe_cfg_fits(dpipe, g)) {
+    kind = 1;
+    idx = dpipe;
+    rows_per_block = pipe_rows_per_block(idx, Epi::kMats);
+  } else if (T <= kStreamMaxLaneTiles) {
+    idx = pick_decode(T, smax, Epi::kMats, g.nseg, (g.col_tiles >> 1) / smax);
+    if (g_forced_cfg >= 0 && decode_cfg_fits(kDecodeCfgs[g_forced_cfg], g, smax, Epi::kMats, Epi::kReduce)) idx = g_forced_cfg;
+    if (!decode_cfg_fits(kDecodeCfgs[idx], g, smax, Epi::kMats, Epi::kReduce)) {
       // fall back to a register-only in-workgroup configuration with a wave per split
       idx = smax == 1 ? 3 : (smax == 2 ? 2 : (smax <= 8 ? 0 : 18));
     }
@@ -351,13 +437,20 @@ int run(Geometry g, const typename Epi::Out& o_in, hipStream_t st) {
     o.cand = nullptr;
     if (kind != 2 && g.nseg == 1) {
       nrb = (g.seg[0].row_tiles + rows_per_block - 1) / rows_per_block;
-      if (static_cast<int64_t>(nrb) * g.rows <= kCandSlots) o.cand = cand_scratch();
+      if (static_cast<int64_t>(nrb) * g.rows <= kCandSlots) o.cand = scratch_base();
       if (!o.cand) nrb = 0;
       o.nrb = nrb;
     }
   }
   if (kind == 0) {
     g_last_cfg = idx;
+    const bool xs = kDecodeCfgs[idx].xs;
+    if (xs) {
+      g.part = reinterpret_cast<float*>(scratch_base());
+      g.split_cnt = split_counters();
+      g.part_splits = smax;
+      if (!g.part || !g.split_cnt) return fail(STRIDE_TC_EINVAL, "split scratch unavailable");
+    }
     launch_decode_cfg<Epi>(idx, g, o, st);
   } else if (kind == 1) {
     g_last_cfg = -3 - idx;
@@ -410,11 +503,12 @@ extern "C" {
 int stride_tc_set_stream_config(int32_t index) {
   if (index <= -3 && -3 - index < kNumPipeCfgs) {
     g_forced_pipe = -3 - index;
+    g_forced_cfg = -1;
     return 0;
   }
   if (index < -1 || index >= kNumDecodeCfgs) return fail(STRIDE_TC_EINVAL, "config index out of range");
   g_forced_cfg = index;
-  if (index == -1) g_forced_pipe = -1;
+  g_forced_pipe = -1;
   return 0;
 }
 
@@ -430,7 +524,7 @@ int stride_tc_stream_config(int32_t index, int32_t* out6) {
   out6[2] = c.ws;
   out6[3] = c.wr;
   out6[4] = c.u;
-  out6[5] = c.xl ? 1 : 0;
+  out6[5] = (c.xl ? 1 : 0) | (c.xs ? 2 : 0);
   return 0;
 }
 

@@ -56,12 +56,8 @@ __global__ __launch_bounds__(kWave * WM * WN, OCC) void k_pipe(Geometry g, typen
   // lane blocks together so that consecutive workgroups (which the hardware puts
   // on one XCD after xcd_remap) share activation tiles in L2.
   int b = xcd_remap(blockIdx.x, gridDim.x);
-  int si = 0;
-  while (si + 1 < g.nseg && b >= g.seg[si].blocks * lblocks) {
-    b -= g.seg[si].blocks * lblocks;
-    ++si;
-  }
-  const Segment& sg = g.seg[si];
+  const int si = locate_segment(g, b, lblocks);
+  const Segment sg = seg_at(g, si);
   constexpr int G = 8;
   const int group = b / (G * lblocks);
   const int gsize = min(G, sg.blocks - group * G);
@@ -86,7 +82,7 @@ __global__ __launch_bounds__(kWave * WM * WN, OCC) void k_pipe(Geometry g, typen
     if (blk < M * BR) {
       const int m = blk / BR;
       const int rt = min(rt0 + blk % BR, sg.row_tiles - 1);
-      base = sg.w[m] + rt * strip;
+      base = (m == 0 ? sg.w[0] : sg.w[1]) + rt * strip;  // no run-time index into sg
     } else {
       const int lt = min(lt0 + blk - M * BR, g.lane_groups - 1);
       base = g.x + lt * strip;
@@ -220,14 +216,12 @@ __global__ __launch_bounds__(kWave * WM * WN, OCC) void k_pipe(Geometry g, typen
     }
     return;
   }
-#pragma unroll
-  for (int r = 0; r < WRT; ++r) {
+  unroll<WRT>([&](auto r) {
     const int rt = rt0 + wr * WRT + r;
-    if (rt >= sg.row_tiles) continue;
-#pragma unroll
-    for (int l = 0; l < WLT; ++l) {
+    if (rt >= sg.row_tiles) return;
+    unroll<WLT>([&](auto l) {
       const int lt = lt0 + wn * WLT + l;
-      if (lt >= g.lane_groups) continue;
+      if (lt >= g.lane_groups) return;
       f32x4 t[M];
 #pragma unroll
       for (int m = 0; m < M; ++m) {
@@ -235,8 +229,8 @@ __global__ __launch_bounds__(kWave * WM * WN, OCC) void k_pipe(Geometry g, typen
         else t[m] = acc[m][r][l];
       }
       Epi::apply(o, g, si, rt, lt, t, lane);
-    }
-  }
+    });
+  });
 }
 
 }  // namespace stride_tc

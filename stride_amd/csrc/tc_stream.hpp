@@ -20,8 +20,12 @@
 
 namespace stride_tc {
 
-template <class Epi, int R, int LT, int WS, int WR, int UC, bool XLC>
+// Largest split count served by cross-workgroup split launches (XS).
+constexpr int kMaxXSplits = 8;
+
+template <class Epi, int R, int LT, int WS, int WR, int UC, bool XLC, bool XS>
 __global__ __launch_bounds__(kWave * WS * WR) void k_stream(Geometry g, typename Epi::Out o) {
+  static_assert(!XS || (WS == 1 && !Epi::kReduce), "cross-workgroup splits use one split group and a plain epilogue");
   constexpr int M = Epi::kMats;
   // UC counts weight chunks in flight per batch; a paired GEMM loads M chunks per step.
   constexpr int U0 = UC / M > 0 ? UC / M : 1;
@@ -53,8 +57,25 @@ __global__ __launch_bounds__(kWave * WS * WR) void k_stream(Geometry g, typename
   const int b = xcd_remap(blockIdx.x, gridDim.x);
   int rb = b / lgroups;
   const int lt0 = (b % lgroups) * LT;
-  const int si = locate_segment(g, rb);
-  const Segment& sg = g.seg[si];
+  int si = 0, xsplit = 0;
+  if constexpr (XS) {
+    // Block -> (segment, split, row block, lane group), row blocks fastest, so
+    // that neighbouring workgroups (one XCD after xcd_remap) read the same
+    // activation chunks.
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      if (si == k && k + 1 < g.nseg && rb >= g.seg[k].blocks * g.seg[k].splits) {
+        rb -= g.seg[k].blocks * g.seg[k].splits;
+        si = k + 1;
+      }
+    }
+    const int bps = seg_at(g, si).blocks;
+    xsplit = rb / bps;
+    rb -= xsplit * bps;
+  } else {
+    si = locate_segment(g, rb);
+  }
+  const Segment sg = seg_at(g, si);
   const int rt_first = rb * (WR * R) + wr * R;
   const int nlt = min(LT, g.lane_groups - lt0);
   const int chunks = g.col_tiles >> 1;
@@ -62,7 +83,8 @@ __global__ __launch_bounds__(kWave * WS * WR) void k_stream(Geometry g, typename
   const int per = chunks / splits;
   const int off = frag_offset(lane);
   const int64_t strip = static_cast<int64_t>(g.col_tiles) * kTileElems;
-  const bool active = ws < splits;
+  const bool active = XS || ws < splits;
+  const int my_split = XS ? xsplit : ws;
 
   const char* wp[M][R];
 #pragma unroll
@@ -102,7 +124,7 @@ __global__ __launch_bounds__(kWave * WS * WR) void k_stream(Geometry g, typename
       for (int l = 0; l < LT; ++l) {
         acc[m][r][l] = f32x4{0.f, 0.f, 0.f, 0.f};
         if constexpr (Epi::kInitFromOutput) {
-          if (ws == 0 && l < nlt && rt_first + r < sg.row_tiles) acc[m][r][l] = Epi::init(o, rt_first + r, lt0 + l, lane);
+          if (my_split == 0 && l < nlt && rt_first + r < sg.row_tiles) acc[m][r][l] = Epi::init(o, rt_first + r, lt0 + l, lane);
         }
       }
 
@@ -112,7 +134,7 @@ __global__ __launch_bounds__(kWave * WS * WR) void k_stream(Geometry g, typename
   // MFMAs must be scalar branches, because an MFMA ignores the EXEC mask and
   // would still accumulate inside an exec-masked block the compiler chose not
   // to branch around.
-  const int c0 = __builtin_amdgcn_readfirstlane(active ? ws * per : 0);
+  const int c0 = __builtin_amdgcn_readfirstlane(active ? my_split * per : 0);
   const int c1 = __builtin_amdgcn_readfirstlane(active ? c0 + per : 0);
   const int nbatch = (c1 - c0) / U;
   const int cb = c0 + nbatch * U;  // batched range [c0, cb), then single chunks up to c1
@@ -224,7 +246,105 @@ __global__ __launch_bounds__(kWave * WS * WR) void k_stream(Geometry g, typename
     }
   }
 
-  if constexpr (Epi::kReduce) {
+  if constexpr (XS) {
+    // One split of each tile. With a single split, finish here. Otherwise every
+    // workgroup of a (row block, lane group) unit publishes its partial tiles
+    // with device-coherent stores and counts itself in; the last one to arrive
+    // folds the splits in ascending order, applies the epilogue and re-arms the
+    // counter for the next launch. Nothing waits on another workgroup.
+    int tile0 = 0, unit0 = 0;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      if (i < si) {
+        tile0 += g.seg[i].row_tiles * g.lane_groups;
+        unit0 += g.seg[i].blocks;
+      }
+    }
+    if (splits == 1) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        if (rt_first + r >= sg.row_tiles) continue;
+#pragma unroll
+        for (int l = 0; l < LT; ++l) {
+          if (l >= nlt) continue;
+          f32x4 y[M];
+#pragma unroll
+          for (int m = 0; m < M; ++m) y[m] = acc[m][r][l];
+          Epi::apply(o, g, si, rt_first + r, lt0 + l, y, lane);
+        }
+      }
+    } else {
+      auto slot = [&](int r, int l, int s, int m) {
+        const int64_t tile = tile0 + static_cast<int64_t>(rt_first + r) * g.lane_groups + lt0 + l;
+        return reinterpret_cast<uint64_t*>(g.part) + ((tile * g.part_splits + s) * M + m) * (2 * kWave) + 2 * lane;
+      };
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        if (rt_first + r >= sg.row_tiles) continue;
+#pragma unroll
+        for (int l = 0; l < LT; ++l) {
+          if (l >= nlt) continue;
+#pragma unroll
+          for (int m = 0; m < M; ++m) {
+            uint64_t* p = slot(r, l, my_split, m);
+            const f32x4 v = acc[m][r][l];
+            __hip_atomic_store(p, static_cast<uint64_t>(u32_of(v[0])) | (static_cast<uint64_t>(u32_of(v[1])) << 32),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(p + 1, static_cast<uint64_t>(u32_of(v[2])) | (static_cast<uint64_t>(u32_of(v[3])) << 32),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
+        }
+      }
+      // The partial stores are complete (performed at device scope) before this
+      // workgroup is counted.
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      __shared__ int last;
+      int* cnt = g.split_cnt + static_cast<int64_t>(unit0 + rb) * lgroups + (lt0 / LT);
+      if (threadIdx.x == 0) {
+        const int before = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last = before == splits - 1;
+        if (last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      __syncthreads();
+      if (last) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          if (rt_first + r >= sg.row_tiles) continue;
+#pragma unroll
+          for (int l = 0; l < LT; ++l) {
+            if (l >= nlt) continue;
+            // Issue every partial load first (at most kMaxXSplits splits, a
+            // wave-uniform bound), then fold in ascending split order.
+            f32x4 part[kMaxXSplits][M];
+#pragma unroll
+            for (int s = 0; s < kMaxXSplits; ++s) {
+              if (s >= splits || s == my_split) continue;
+#pragma unroll
+              for (int m = 0; m < M; ++m) {
+                const uint64_t* p = slot(r, l, s, m);
+                const uint64_t lo = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const uint64_t hi = __hip_atomic_load(p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                part[s][m] = f32x4{f32_of(static_cast<uint32_t>(lo)), f32_of(static_cast<uint32_t>(lo >> 32)),
+                                   f32_of(static_cast<uint32_t>(hi)), f32_of(static_cast<uint32_t>(hi >> 32))};
+              }
+            }
+            f32x4 y[M];
+#pragma unroll
+            for (int s = 0; s < kMaxXSplits; ++s) {
+              if (s >= splits) continue;
+#pragma unroll
+              for (int m = 0; m < M; ++m) {
+                const f32x4 v = s == my_split ? acc[m][r][l] : part[s][m];
+                y[m] = s == 0 ? v : y[m] + v;
+              }
+            }
+            Epi::apply(o, g, si, rt_first + r, lt0 + l, y, lane);
+          }
+        }
+      }
+    }
+  } else if constexpr (Epi::kReduce) {
     // Candidates of every tile this workgroup owns are merged first; then one
     // wave publishes a single update per batch lane.
     float bv[LT];

@@ -25,7 +25,7 @@ __global__ __launch_bounds__(256) void k_tile(Geometry g, typename Epi::Out o) {
   int rb = b / lblocks;
   const int lt0 = (b % lblocks) * BL;
   const int si = locate_segment(g, rb);
-  const Segment& sg = g.seg[si];
+  const Segment sg = seg_at(g, si);
   const int rt0 = rb * BR;
   const int chunks = g.col_tiles >> 1;
   const int per = chunks / sg.splits;

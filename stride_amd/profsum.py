@@ -2,15 +2,21 @@
 
     python -m stride_amd.profsum kernels <kernel_trace.csv> [--match k_] > summary.txt
     python -m stride_amd.profsum counters <counter_collection.csv> [--match k_]
+    python -m stride_amd.profsum traffic <fetch counter_collection.csv> --write-csv <write csv> \
+        --calib-match neg --calib-bytes 536870912 > traffic.json
 
 `kernels` prints count / average / min / max duration (us) per kernel name, as
 rocprofv3 --stats does; `counters` prints the average value per dispatch of each
-counter per kernel (FETCH_SIZE and WRITE_SIZE are in KiB).
+counter per kernel (FETCH_SIZE and WRITE_SIZE are in KiB). `traffic` turns a
+FETCH_SIZE run and a WRITE_SIZE run into HBM bytes per dispatch, each counter
+scaled by what it reads for a calibration kernel that moves a known number of
+bytes each way (a plain copy), and prints the JSON that bench.py reads.
 """
 from __future__ import annotations
 
 import argparse
 import csv
+import json
 import re
 import sys
 from collections import defaultdict
@@ -54,13 +60,55 @@ def counters(path: str, match: str | None) -> None:
             print(f"{n:<90} {c:>12} {k:>10} {vals[n][c] / k:>18.1f}")
 
 
+def per_dispatch(path: str, counter: str) -> dict:
+    """Average value of `counter` per dispatch, by short kernel name."""
+    vals = defaultdict(float)
+    disp = defaultdict(set)
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            if r["Counter_Name"] != counter:
+                continue
+            n = short(r["Kernel_Name"])
+            vals[n] += float(r["Counter_Value"])
+            disp[n].add(r["Dispatch_Id"])
+    return {n: vals[n] / len(disp[n]) for n in vals}
+
+
+def traffic(fetch_csv: str, write_csv: str, calib_match: str, calib_bytes: int, match: str | None) -> None:
+    fetch = per_dispatch(fetch_csv, "FETCH_SIZE")
+    write = per_dispatch(write_csv, "WRITE_SIZE")
+    cal = [n for n in fetch if calib_match in n]
+    if len(cal) != 1 or cal[0] not in write:
+        raise SystemExit(f"need exactly one calibration kernel matching {calib_match!r} in both runs, found {cal}")
+    fs = calib_bytes / (fetch[cal[0]] * 1024.0)
+    ws = calib_bytes / (write[cal[0]] * 1024.0)
+    out = {
+        "source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE --kernel-trace, one run each",
+        "calibration": {"kernel": cal[0], "bytes_each_way": calib_bytes, "fetch_scale": round(fs, 4),
+                        "write_scale": round(ws, 4)},
+        "kernels": {},
+    }
+    for n in sorted(fetch):
+        if n == cal[0] or (match and match not in n) or n not in write:
+            continue
+        fb, wb = fetch[n] * 1024.0 * fs, write[n] * 1024.0 * ws
+        out["kernels"][n] = {"fetch_bytes": int(fb), "write_bytes": int(wb), "hbm_bytes": int(fb + wb)}
+    print(json.dumps(out, indent=1))
+
+
 def main(argv=None) -> None:
     ap = argparse.ArgumentParser()
-    ap.add_argument("mode", choices=["kernels", "counters"])
+    ap.add_argument("mode", choices=["kernels", "counters", "traffic"])
     ap.add_argument("csv")
     ap.add_argument("--match", default=None)
+    ap.add_argument("--write-csv", default=None)
+    ap.add_argument("--calib-match", default="neg")
+    ap.add_argument("--calib-bytes", type=int, default=512 << 20)
     a = ap.parse_args(argv)
-    (kernels if a.mode == "kernels" else counters)(a.csv, a.match)
+    if a.mode == "traffic":
+        traffic(a.csv, a.write_csv, a.calib_match, a.calib_bytes, a.match)
+    else:
+        (kernels if a.mode == "kernels" else counters)(a.csv, a.match)
 
 
 if __name__ == "__main__":

@@ -8,8 +8,14 @@ adds a chunk twice. Every k-loop must therefore guard MFMAs with scalar
 (wave-uniform) branches only; this test disassembles the built library and
 fails if any MFMA is reachable, in straight-line order, after an EXEC
 narrowing with no `s_cbranch_execz` in between.
+
+Second check: every LDS-pipelined kernel (k_pipe) must use exactly the LDS of
+its staging ring, NS stages x (mats*WM*WRT + WN*WLT) tiles x KC chunks x 1 KiB.
+Anything more is a private copy the compiler moved into LDS (a local struct
+indexed at run time), which costs LDS capacity and an LDS round trip per use.
 """
 import os
+import re
 import struct
 import subprocess
 import tempfile
@@ -93,3 +99,39 @@ def test_no_mfma_under_exec_mask(lib):
     assert "v_mfma" in dis
     bad = masked_mfmas(dis)
     assert not bad, f"{len(bad)} MFMAs under an exec mask, first in {bad[0][0]}"
+
+
+def kernel_lds(co_path: str):
+    """(kernel name, group segment bytes) from the code object's metadata note."""
+    notes = subprocess.run([OBJDUMP.replace("llvm-objdump", "llvm-readelf"), "--notes", co_path],
+                           capture_output=True, text=True, check=True).stdout
+    out, grp = [], None
+    for line in notes.splitlines():
+        line = line.strip()
+        if line.startswith(".group_segment_fixed_size:"):
+            grp = int(line.split()[-1])
+        elif line.startswith(".name:"):
+            out.append((line.split()[-1], grp))
+    return out
+
+
+def test_pipe_lds_is_exactly_the_ring():
+    path = os.path.join(PKG, "libstride_tc.so")
+    if not os.path.exists(path):
+        pytest.skip("libstride_tc.so not built")
+    if not os.path.exists(OBJDUMP):
+        pytest.skip("llvm tools not available")
+    with tempfile.TemporaryDirectory() as d:
+        co = os.path.join(d, "k.co")
+        open(co, "wb").write(code_object(path))
+        kernels = kernel_lds(co)
+    seen = 0
+    for name, grp in kernels:
+        m = re.search(r"k_pipeINS_\d+(\w+?)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELb(\d)", name)
+        if not m:
+            continue
+        wrt, wlt, wm, wn, kc, ns, _ = map(int, m.groups()[1:8])
+        mats = 2 if m.group(1) == "EpiGateUp" else 1
+        assert grp == ns * (mats * wm * wrt + wn * wlt) * kc * 1024, f"{name}: {grp} bytes of LDS"
+        seen += 1
+    assert seen > 0
