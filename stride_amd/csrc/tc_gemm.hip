@@ -279,15 +279,6 @@ int pick_decode(int T, int smax, int mats, int nseg, int per) {
   return smax == 1 ? 16 : (smax == 2 ? 36 : (nseg == 3 ? 9 : 33));
 }
 
-// Decode batches for which the LDS-pipelined kernel with small blocks measured
-// faster: the LM head (one split) from two lane tiles up and the paired gate/up
-// GEMM from four. Returns a prefill configuration index or -1.
-int pick_decode_pipe(int T, int smax, int mats) {
-  if (smax == 1 && T >= 2) return T <= 4 ? 14 : 8;
-  if (smax == 2 && mats == 2 && T >= 3) return T <= 4 ? 17 : 15;
-  return -1;
-}
-
 template <class Epi, int WRT, int WLT>
 int launch_tile(Geometry g, const typename Epi::Out& o, hipStream_t st) {
   int blocks = 0;
@@ -398,6 +389,53 @@ int pipe_rows_per_block(int idx, int mats) {
   return wm[idx] * r;
 }
 
+// Automatic choice of kernel family and configuration, from measured sweeps on
+// MI355X (HIP-graph timing, weights rotated past the MALL; every choice computes
+// the same bits). kind 0: k_stream configuration, kind 1: k_pipe configuration.
+struct Pick {
+  int kind, idx;
+};
+
+// At most 8 lane tiles. The LDS-pipelined kernel with small blocks wins for the
+// LM head from two lane tiles up and for the paired gate/up GEMM from three.
+Pick pick_small(int T, int smax, int mats, int nseg, int per) {
+  if (smax == 1 && T >= 2) return {1, T <= 4 ? 14 : 8};
+  if (smax == 2 && mats == 2 && T >= 3) return {1, T <= 4 ? 17 : 15};
+  return {0, pick_decode(T, smax, mats, nseg, per)};
+}
+
+// More than 8 lane tiles. Matrices with eight splits (QKV, O, down) have few row
+// tiles and long split chains: up to a few hundred rows the streaming kernel,
+// whose waves run the splits side by side, beats the pipeline, which walks them
+// one after another; beyond, the pipeline with a block shape per size.
+Pick pick_large(const Geometry& g, int T, int smax, int per) {
+  if (smax == 1) return {1, T <= 12 || T > 24 ? 3 : 8};
+  if (smax == 2) {
+    if (T <= 12) return {1, 12};
+    if (T <= 24) return {1, 8};
+    if (T <= 48) return {1, 2};
+    return {1, pick_pipe(g, smax)};
+  }
+  if (g.nseg == 3) {  // fused QKV
+    if (T <= 12) return {0, 33};
+    if (T <= 24) return {0, 29};
+    if (T <= 64) return {1, 12};
+    return {1, 2};
+  }
+  if (per >= 32) {  // long splits (down)
+    if (T <= 12) return {0, 27};
+    if (T <= 32) return {0, 29};
+    if (T <= 64) return {0, 30};
+    return {1, pick_pipe(g, smax)};
+  }
+  if (T <= 12) return {0, 27};
+  if (T <= 32) return {0, 29};
+  if (T <= 64) return {1, 12};
+  if (T <= 96) return {1, 14};
+  if (T <= 128) return {1, 0};
+  return {1, 2};
+}
+
 template <class Epi>
 int run(Geometry g, const typename Epi::Out& o_in, hipStream_t st) {
   if (g.rows == 0) return 0;
@@ -408,29 +446,32 @@ int run(Geometry g, const typename Epi::Out& o_in, hipStream_t st) {
     smax = g.seg[i].splits > smax ? g.seg[i].splits : smax;
   }
   const int T = g.lane_groups;
-  int kind = 0, idx = 0, rows_per_block = 0;  // kind 0: decode, 1: pipe, 2: legacy tile
-  // A forced prefill configuration (tuning hook) also serves decode batches.
-  const int dpipe = g_forced_cfg >= 0 ? -1 : (g_forced_pipe >= 0 ? g_forced_pipe : pick_decode_pipe(T, smax, Epi::kMats));
-  if (T <= kStreamMaxLaneTiles && dpipe >= 0 && pipe_cfg_fits(dpipe, g)) {
+  int kind = 0, idx = 0, rows_per_block = 0;  // kind 0: streaming, 1: pipe, 2: legacy tile
+  const int per = (g.col_tiles >> 1) / smax;
+  const bool forced_stream =
+      g_forced_cfg >= 0 && decode_cfg_fits(kDecodeCfgs[g_forced_cfg], g, smax, Epi::kMats, Epi::kReduce);
+  const bool forced_pipe = g_forced_pipe >= 0 && pipe_cfg_fits(g_forced_pipe, g);
+  if (forced_stream) {
+    idx = g_forced_cfg;
+  } else if (forced_pipe) {
     kind = 1;
-    idx = dpipe;
-    rows_per_block = pipe_rows_per_block(idx, Epi::kMats);
-  } else if (T <= kStreamMaxLaneTiles) {
-    idx = pick_decode(T, smax, Epi::kMats, g.nseg, (g.col_tiles >> 1) / smax);
-    if (g_forced_cfg >= 0 && decode_cfg_fits(kDecodeCfgs[g_forced_cfg], g, smax, Epi::kMats, Epi::kReduce)) idx = g_forced_cfg;
-    if (!decode_cfg_fits(kDecodeCfgs[idx], g, smax, Epi::kMats, Epi::kReduce)) {
-      // fall back to a register-only in-workgroup configuration with a wave per split
+    idx = g_forced_pipe;
+  } else {
+    const Pick p = T <= kStreamMaxLaneTiles ? pick_small(T, smax, Epi::kMats, g.nseg, per) : pick_large(g, T, smax, per);
+    kind = p.kind;
+    idx = p.idx;
+    if (kind == 1 && !pipe_cfg_fits(idx, g)) {
+      idx = pick_pipe(g, smax);
+      if (!pipe_cfg_fits(idx, g)) idx = 0;
+      if (!pipe_cfg_fits(idx, g)) kind = 2;
+    }
+    if (kind == 0 && !decode_cfg_fits(kDecodeCfgs[idx], g, smax, Epi::kMats, Epi::kReduce)) {
+      // a register-only in-workgroup configuration with a wave per split always fits
       idx = smax == 1 ? 3 : (smax == 2 ? 2 : (smax <= 8 ? 0 : 18));
     }
-    rows_per_block = kDecodeCfgs[idx].wr * kDecodeCfgs[idx].r;
-  } else {
-    kind = 1;
-    idx = pick_pipe(g, smax);
-    if (g_forced_pipe >= 0) idx = g_forced_pipe;
-    if (!pipe_cfg_fits(idx, g)) idx = 0;
-    if (!pipe_cfg_fits(idx, g)) kind = 2;
-    else rows_per_block = pipe_rows_per_block(idx, Epi::kMats);
   }
+  if (kind == 0) rows_per_block = kDecodeCfgs[idx].wr * kDecodeCfgs[idx].r;
+  if (kind == 1) rows_per_block = pipe_rows_per_block(idx, Epi::kMats);
   // Greedy LM head: two passes through the candidate scratch when it fits.
   int nrb = 0;
   if constexpr (Epi::kReduce) {
