@@ -13,19 +13,24 @@
 // y = ((c0 + c1) + c2) + ... + c(S-1), then the epilogue. The reference fixes the
 // same kind of tree with kFewRowsWarps (src/kernels_tc.cu:29-32, 462-496).
 //
-// Two kernel families evaluate that expression:
-//   k_stream  decode regime (at most 8 lane tiles, M <= 128): weight-streaming.
-//             A workgroup owns WR*R row tiles and up to LT lane tiles; its waves
-//             split the K range (WS waves along K), stream weight chunks straight
-//             from HBM into registers with 16-byte loads, and combine the S split
-//             partials through LDS in ascending split order.
-//   k_tile    prefill regime (more than 8 lane tiles): an LDS-staged block GEMM.
-//             A 2x2-wave workgroup owns a (2*WRT) x (2*WLT) block of tiles; each
-//             32-column chunk of weights and activations is staged through a
-//             double-buffered LDS ring, and each wave walks the splits in order,
-//             folding a finished split into its running sum in registers.
-// Both call the same chunk order, the same MFMA instruction and the same
-// epilogue functions, so every output row has the same bits for any M.
+// Kernel families evaluating that expression (tc_stream.hpp, tc_pipe.hpp):
+//   k_stream  weight streaming. A workgroup owns WR*R row tiles and LT lane
+//             tiles; its WS split waves run the splits side by side, stream
+//             weight chunks straight from HBM into registers with 16-byte loads,
+//             and combine the split partials through LDS in ascending order. With
+//             XS, each workgroup runs one split and the last one to finish a tile
+//             group folds the partials in order. Serves decode batches and, for
+//             matrices with eight splits, prefill up to about a thousand rows.
+//   k_pipe    LDS pipeline. WM x WN waves own a block of tiles; every stage's
+//             chunks are copied HBM->LDS by global_load_lds in fragment order
+//             through an NS-deep ring; splits are walked in order and folded in
+//             registers. Serves prefill, and with small blocks the LM head and
+//             gate/up from two to eight lane tiles.
+//   k_tile    the first LDS-staged kernel, kept as the fallback when a split
+//             length is not a multiple of the pipeline's chunks per stage.
+// All call the same chunk order, the same MFMA instruction and the same
+// epilogue functions, so every output row has the same bits for any M and any
+// configuration; run() picks the configuration from measured sweeps.
 #include <hip/hip_runtime.h>
 
 #include <cstdio>
