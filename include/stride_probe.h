@@ -32,6 +32,14 @@ int stride_probe_mfma_rate_variant(float* out, int32_t blocks, int32_t iters, in
  * per workgroup to out[blocks]. blocks = 0 picks one workgroup per 64 KiB. */
 int stride_probe_read(const void* buf, int64_t bytes, uint32_t* out, int32_t blocks, int32_t unroll, void* stream);
 
+/* Equivalence of the two bf16 MFMA shapes: for each of `cases` 32x32 output
+ * blocks chained over `chunks` 32-column chunks from c0, o16 receives the result
+ * of v_mfma_f32_16x16x32_bf16 (one per 16x16 sub-block and chunk) and o32 that of
+ * v_mfma_f32_32x32x16_bf16 (two per chunk). a: [cases][32][32*chunks] bf16,
+ * b: [cases][32][32*chunks] bf16, c0/o16/o32: [cases][32][32] fp32. */
+int stride_probe_mfma_equiv(const uint16_t* a, const uint16_t* b, const float* c0, float* o16, float* o32,
+                            int32_t cases, int32_t chunks, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -162,6 +162,8 @@ int stride_tc_split_count(int32_t n, int32_t k);
  * launch is ignored for it. */
 int stride_tc_set_stream_config(int32_t index);
 int stride_tc_stream_config_count(void);
+/* Number of LDS-pipelined configurations (selected as -3-i above). */
+int stride_tc_pipe_config_count(void);
 /* Configuration used by the last launch in this process (-2: the prefill
  * kernel, -1: none yet). */
 int stride_tc_last_stream_config(void);

@@ -87,6 +87,7 @@ EXPORTS = (
     "stride_tc_version",
     "stride_tc_set_stream_config",
     "stride_tc_stream_config_count",
+    "stride_tc_pipe_config_count",
     "stride_tc_stream_config",
     "stride_tc_last_stream_config",
 )
@@ -138,6 +139,8 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     lib.stride_tc_set_stream_config.restype = C.c_int
     lib.stride_tc_stream_config_count.argtypes = []
     lib.stride_tc_stream_config_count.restype = C.c_int
+    lib.stride_tc_pipe_config_count.argtypes = []
+    lib.stride_tc_pipe_config_count.restype = C.c_int
     lib.stride_tc_stream_config.argtypes = [C.c_int32, C.POINTER(C.c_int32)]
     lib.stride_tc_stream_config.restype = C.c_int
     lib.stride_tc_last_stream_config.argtypes = []
@@ -162,6 +165,11 @@ def split_count(n: int, k: int) -> int:
     if s < 0:
         check(s)
     return s
+
+
+def pipe_config_count() -> int:
+    """Number of LDS-pipelined kernel configurations (forced as -3 - i)."""
+    return load().stride_tc_pipe_config_count()
 
 
 def stream_configs():

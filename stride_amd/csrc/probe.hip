@@ -146,3 +146,56 @@ extern "C" int stride_probe_read(const void* buf, int64_t bytes, uint32_t* out, 
   }
   return static_cast<int>(hipGetLastError());
 }
+
+// Equivalence of the two bf16 MFMA shapes on one 32x32 output block chained
+// over `chunks` 32-column chunks from the initial value c0: (a) four
+// v_mfma_f32_16x16x32_bf16, one per 16x16 sub-block and chunk; (b) two
+// v_mfma_f32_32x32x16_bf16 per chunk (columns 0-15, then 16-31). a is
+// [32 rows][32*chunks] bf16 row-major, b is [32 lanes][32*chunks], c0 and both
+// outputs [32 rows][32 lanes] fp32. One block of 64 threads per test case.
+__global__ __launch_bounds__(64) void k_mfma_equiv(const uint16_t* a, const uint16_t* b, const float* c0, float* o16,
+                                                   float* o32, int chunks) {
+  const int lane = threadIdx.x;
+  const int t = blockIdx.x;
+  const int kk = 32 * chunks;
+  a += static_cast<int64_t>(t) * 32 * kk;
+  b += static_cast<int64_t>(t) * 32 * kk;
+  c0 += t * 1024;
+  o16 += t * 1024;
+  o32 += t * 1024;
+  auto frag = [&](const uint16_t* m, int row, int k) {
+    u32x4 v;
+    const uint32_t* p = reinterpret_cast<const uint32_t*>(m + static_cast<int64_t>(row) * kk + k);
+    v[0] = p[0]; v[1] = p[1]; v[2] = p[2]; v[3] = p[3];
+    return v;
+  };
+  // (a) 16x16x32: C lane l holds lane column l%16, rows 4*(l/16)+i.
+  for (int rb = 0; rb < 2; ++rb)
+    for (int cb = 0; cb < 2; ++cb) {
+      f32x4 acc;
+      for (int i = 0; i < 4; ++i) acc[i] = c0[(rb * 16 + 4 * (lane / 16) + i) * 32 + cb * 16 + lane % 16];
+      for (int c = 0; c < chunks; ++c) {
+        const u32x4 fa = frag(a, rb * 16 + lane % 16, 32 * c + 8 * (lane / 16));
+        const u32x4 fb = frag(b, cb * 16 + lane % 16, 32 * c + 8 * (lane / 16));
+        acc = mfma(fa, fb, acc);
+      }
+      for (int i = 0; i < 4; ++i) o16[(rb * 16 + 4 * (lane / 16) + i) * 32 + cb * 16 + lane % 16] = acc[i];
+    }
+  // (b) 32x32x16: C lane l holds lane column l%32, rows 8*(i/4) + 4*(l/32) + i%4.
+  f32x16 acc;
+  for (int i = 0; i < 16; ++i) acc[i] = c0[(8 * (i / 4) + 4 * (lane / 32) + i % 4) * 32 + lane % 32];
+  for (int c = 0; c < chunks; ++c)
+    for (int h = 0; h < 2; ++h) {
+      const u32x4 fa = frag(a, lane % 32, 32 * c + 16 * h + 8 * (lane / 32));
+      const u32x4 fb = frag(b, lane % 32, 32 * c + 16 * h + 8 * (lane / 32));
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(fa), as_bf16x8(fb), acc, 0, 0, 0);
+    }
+  for (int i = 0; i < 16; ++i) o32[(8 * (i / 4) + 4 * (lane / 32) + i % 4) * 32 + lane % 32] = acc[i];
+}
+
+extern "C" int stride_probe_mfma_equiv(const uint16_t* a, const uint16_t* b, const float* c0, float* o16, float* o32,
+                                       int32_t cases, int32_t chunks, void* stream) {
+  if (cases <= 0 || chunks <= 0) return 1;
+  hipLaunchKernelGGL(k_mfma_equiv, dim3(cases), dim3(64), 0, static_cast<hipStream_t>(stream), a, b, c0, o16, o32, chunks);
+  return static_cast<int>(hipGetLastError());
+}

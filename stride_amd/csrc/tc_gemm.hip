@@ -332,9 +332,17 @@ void launch_pipe(Geometry g, const typename Epi::Out& o, int smax, hipStream_t s
   X(14, 4, 1, 1, 4, 2, 4, 1)      \
   X(15, 2, 2, 1, 4, 2, 4, 2)      \
   X(16, 4, 2, 2, 2, 2, 4, 1)      \
-  X(17, 4, 1, 1, 4, 2, 6, 1)
+  X(17, 4, 1, 1, 4, 2, 6, 1)       \
+  X(18, 4, 8, 4, 2, 1, 4, 1)      \
+  X(19, 4, 8, 4, 2, 1, 5, 1)      \
+  X(20, 8, 4, 2, 4, 1, 4, 1)      \
+  X(21, 4, 4, 4, 2, 1, 5, 1)      \
+  X(22, 4, 4, 4, 2, 1, 6, 1)      \
+  X(23, 4, 4, 2, 4, 1, 5, 1)      \
+  X(24, 8, 8, 2, 2, 1, 4, 1)      \
+  X(25, 4, 8, 2, 2, 1, 6, 1)
 
-constexpr int kNumPipeCfgs = 18;
+constexpr int kNumPipeCfgs = 26;
 int g_forced_pipe = -1;
 
 template <class Epi>
@@ -370,8 +378,10 @@ bool pipe_cfg_fits(int idx, const Geometry& g) {
 #undef STRIDE_TC_PIPE_KC
   };
   const int chunks = g.col_tiles >> 1;
+  // An odd chunk count per stage is processed two stages at a time.
+  const int step = kc[idx] % 2 ? 2 * kc[idx] : kc[idx];
   for (int i = 0; i < g.nseg; ++i)
-    if ((chunks / g.seg[i].splits) % kc[idx] != 0) return false;
+    if ((chunks / g.seg[i].splits) % step != 0) return false;
   return true;
 }
 
@@ -559,6 +569,8 @@ int stride_tc_set_stream_config(int32_t index) {
 }
 
 int stride_tc_stream_config_count(void) { return kNumDecodeCfgs; }
+
+int stride_tc_pipe_config_count(void) { return kNumPipeCfgs; }
 
 int stride_tc_last_stream_config(void) { return g_last_cfg; }
 

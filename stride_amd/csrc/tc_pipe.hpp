@@ -35,6 +35,8 @@ namespace stride_tc {
 constexpr int vmcnt_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
 // The same with lgkmcnt = 0 (all LDS reads of this wave returned).
 constexpr int vm_lgkm0_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4); }
+// lgkmcnt = 0 only (vmcnt and expcnt at their no-wait maxima).
+constexpr int lgkm0_imm() { return vmcnt_imm(63) & ~(0xF << 8); }
 
 template <class Epi, int WRT, int WLT, int WM, int WN, int KC, int NS, int OCC, bool HASY>
 __global__ __launch_bounds__(kWave * WM * WN, OCC) void k_pipe(Geometry g, typename Epi::Out o) {
@@ -99,7 +101,11 @@ __global__ __launch_bounds__(kWave * WM * WN, OCC) void k_pipe(Geometry g, typen
     }
   };
 
-  static_assert(KC % 2 == 0, "fragment double buffering assumes an even chunk count per stage");
+  // Fragments are double-buffered by chunk parity. With an odd chunk count per
+  // stage the parity flips from stage to stage, so stages are processed in pairs
+  // (the host only selects such a configuration when every split has an even
+  // number of stages).
+  constexpr bool kPairStages = KC % 2 != 0;
   f32x4 acc[M][WRT][WLT];
   f32x4 y[HASY ? M : 1][HASY ? WRT : 1][HASY ? WLT : 1];
   u32x4 fa[2][M][WRT], fb[2][WLT];  // fragments of the current and the next chunk
@@ -133,23 +139,34 @@ __global__ __launch_bounds__(kWave * WM * WN, OCC) void k_pipe(Geometry g, typen
   // One stage: KC chunks; the fragments of chunk kc+1 are read while chunk kc's
   // MFMAs run. Before the last chunk, the wave waits for stage i+1, hands stage
   // i's slot back to the copy engine and starts reading stage i+1.
-  auto stage = [&](int i) {
+  auto stage = [&](int i, auto parity) {
 #pragma unroll
     for (int kc = 0; kc < KC; ++kc) {
-      const int cur = kc & 1, nxt = cur ^ 1;
-      if (kc + 1 < KC) {
-        read_frags(nxt, i, kc + 1);
-      } else if (i + 1 < nst) {
+      const int cur = (decltype(parity)::value + kc) & 1, nxt = cur ^ 1;
+      // This step's fragments were read during the previous step.
+      __builtin_amdgcn_s_waitcnt(lgkm0_imm());
+      const bool last = kc + 1 == KC;
+      if (last && i + 1 < nst) {
         sync_for(i + 1);
         if (i + NS < nst) issue(i + NS);
-        read_frags(nxt, i + 1, 0);
       }
+      // Read the next chunk's fragments (after the final chunk: a harmless
+      // re-read of the current stage) in one straight block with this chunk's
+      // MFMAs, interleaved so that LDS reads and the matrix pipe overlap.
+      read_frags(nxt, last ? min(i + 1, nst - 1) : i, last ? 0 : kc + 1);
 #pragma unroll
       for (int l = 0; l < WLT; ++l)
 #pragma unroll
         for (int m = 0; m < M; ++m)
 #pragma unroll
           for (int r = 0; r < WRT; ++r) acc[m][r][l] = mfma(fa[cur][m][r], fb[cur][l], acc[m][r][l]);
+      constexpr int kReads = M * WRT + WLT, kMfma = M * WRT * WLT;
+#pragma unroll
+      for (int q = 0; q < kReads; ++q) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);               // one ds_read
+        __builtin_amdgcn_sched_group_barrier(0x008, kMfma / kReads, 0);  // MFMAs
+      }
+      if constexpr (kMfma % kReads != 0) __builtin_amdgcn_sched_group_barrier(0x008, kMfma % kReads, 0);
     }
   };
 
@@ -168,7 +185,14 @@ __global__ __launch_bounds__(kWave * WM * WN, OCC) void k_pipe(Geometry g, typen
             if (s == 0 && rt < sg.row_tiles && lt < g.lane_groups) acc[m][r][l] = Epi::init(o, rt, lt, lane);
           }
         }
-    for (int j = 0; j < stages_per_split; ++j, ++i) stage(i);
+    if constexpr (kPairStages) {
+      for (int j = 0; j < stages_per_split; j += 2, i += 2) {
+        stage(i, std::integral_constant<int, 0>{});
+        stage(i + 1, std::integral_constant<int, 1>{});
+      }
+    } else {
+      for (int j = 0; j < stages_per_split; ++j, ++i) stage(i, std::integral_constant<int, 0>{});
+    }
     if constexpr (HASY) {
 #pragma unroll
       for (int m = 0; m < M; ++m)

@@ -25,6 +25,8 @@ def load():
         lib.stride_probe_mfma_rate.restype = C.c_int
         lib.stride_probe_mfma_rate_variant.argtypes = [vp, C.c_int32, C.c_int32, C.c_int32, vp]
         lib.stride_probe_mfma_rate_variant.restype = C.c_int
+        lib.stride_probe_mfma_equiv.argtypes = [vp, vp, vp, vp, vp, C.c_int32, C.c_int32, vp]
+        lib.stride_probe_mfma_equiv.restype = C.c_int
         _lib = lib
     return _lib
 
@@ -52,3 +54,10 @@ def mfma_rate_variant(out, blocks: int, iters: int, variant: int, stream: int) -
     rc = load().stride_probe_mfma_rate_variant(out.data_ptr(), blocks, iters, variant, stream)
     if rc:
         raise RuntimeError(f"stride_probe_mfma_rate_variant failed ({rc})")
+
+
+def mfma_equiv(a, b, c0, o16, o32, chunks: int, stream: int) -> None:
+    rc = load().stride_probe_mfma_equiv(a.data_ptr(), b.data_ptr(), c0.data_ptr(), o16.data_ptr(), o32.data_ptr(),
+                                        c0.shape[0], chunks, stream)
+    if rc:
+        raise RuntimeError(f"stride_probe_mfma_equiv failed ({rc})")

@@ -73,7 +73,7 @@ def test_all_configs_identical(setup, m):
         _lib.set_stream_config(-1)
 
 
-@pytest.mark.parametrize("m", [150, 290, 1024])
+@pytest.mark.parametrize("m", [20, 128, 150, 290, 1024])
 def test_all_prefill_configs_identical(setup, m):
     """The same for the prefill (LDS-pipelined) kernel configurations; their
     outputs must also match the decode kernels row for row."""
@@ -83,7 +83,7 @@ def test_all_prefill_configs_identical(setup, m):
     _lib.set_stream_config(-1)
     ref = run_all(W, xx, hh, m)
     try:
-        for i in range(10):
+        for i in range(_lib.pipe_config_count()):
             say("prefill config", i, "M =", m)
             _lib.set_stream_config(-3 - i)
             got = run_all(W, xx, hh, m)
