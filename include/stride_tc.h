@@ -122,6 +122,57 @@ typedef struct StrideTcLmFullParams {
   float* logits;
 } StrideTcLmFullParams;
 
+/* src/kernels_tc.h:10-16 */
+typedef struct StrideTcEmbedParams {
+  StrideLanes l;
+  const uint16_t* embed; /* tied embedding as weight tiles [rt][ct][16][16] bf16 */
+  const int32_t* tokens; /* [rows] */
+  float* h;              /* fp32 tiles [lt][ct][16 lanes][16 cols] */
+  int32_t dim;
+} StrideTcEmbedParams;
+
+/* src/kernels_tc.h:18-25 */
+typedef struct StrideTcNormParams {
+  StrideLanes l;
+  const float* h;       /* fp32 tiles [lt][ct][16 lanes][16 cols] */
+  uint16_t* x;          /* bf16 tiles, same grid */
+  const float* weight;  /* [dim] gains */
+  int32_t dim;
+  float eps;
+} StrideTcNormParams;
+
+/* src/kernels_tc.h:55-62 */
+typedef struct StrideTcCompactParams {
+  StrideLanes l;
+  const uint16_t* in;     /* bf16 tiles [lt][ct][16][16] */
+  uint16_t* out;          /* bf16 tiles, lane l = in lane lm_rows[l] */
+  const int32_t* lm_rows;
+  int32_t lm_count;
+  int32_t col_tiles;
+} StrideTcCompactParams;
+
+/* src/kernels.h:79-98 */
+typedef struct StrideAttentionParams {
+  StrideLanes l;
+  const float* q; /* [row][head][dim] fp32 (tc_qkv's q_out) */
+  int32_t q_stride;
+  void* out;      /* bf16 x tiles [lt][ct][16][16], out_cols columns */
+  int32_t out_cols;
+  StrideKvRef kv;
+  const int32_t* row_slot;
+  const int32_t* row_pos;
+  const int32_t* items; /* (row, page) pairs to compute this call */
+  int32_t item_count;
+  float* scratch;       /* caller-owned page records */
+  int32_t max_pages;
+  int32_t rec_floats;   /* >= 8 + 4 * head_dim */
+  int32_t layer;
+  int32_t n_kv;
+  int32_t n_q;
+  int32_t head_dim;
+  float scale;
+} StrideAttentionParams;
+
 /* Replaces stride::tc_qkv (src/kernels_tc.h:81, src/kernels_tc.cu:677-679):
  * q = Wq x, k = Wk x, v = Wv x with RoPE on q and k (row tiles hold RoPE pairs
  * (d0+i, d0+D/2+i), src/model.cpp:178-183); q -> fp32 q_out[row*q_stride +
@@ -148,6 +199,30 @@ int stride_tc_lm_greedy(const StrideTcLmGreedyParams* p, int row_tiles_per_warp,
 /* Replaces stride::tc_lm_full (src/kernels_tc.h:87, src/kernels_tc.cu:707-710):
  * logits tiles [row tile][lane tile][16 rows][16 lanes], fp32. */
 int stride_tc_lm_full(const StrideTcLmFullParams* p, int lane_tiles_per_block, void* stream);
+
+/* Replaces stride::tc_embed (src/kernels_tc.h:79, src/kernels_tc.cu:179-203):
+ * h tile row of lane j <- the fp32 widening of embedding row tokens[j]. */
+int stride_tc_embed(const StrideTcEmbedParams* p, void* stream);
+
+/* Replaces stride::tc_norm (src/kernels_tc.h:80, src/kernels_tc.cu:205-340):
+ * x = bf16(weight * (h * r)), r = 1 / sqrtf(sum / dim + eps), where sum is the
+ * reference's fixed tree: 32 partials (partial t = fmaf over the 16 columns of
+ * column tiles ct == t mod 32, ascending), added left to right. per_lane = 0
+ * also writes zeros to the padding lanes of the last lane tile. */
+int stride_tc_norm(const StrideTcNormParams* p, int per_lane, void* stream);
+
+/* Replaces stride::tc_attention (src/kernels_tc.h:82, src/kernels_tc.cu:668-679,
+ * src/kernel_common.h:84-309): paged attention over bf16 KV for groups of four
+ * query heads sharing one KV head. Each (row, 64-position page) item is summed
+ * on its own into a record (max, denominator, weighted values) in `scratch`;
+ * then each row's pages are combined in ascending order and the output is
+ * written as bf16 x tiles. The KV storage page (group_elems / head_dim tokens,
+ * a power of two) is independent of the 64-position summation page. */
+int stride_tc_attention(const StrideAttentionParams* p, void* stream);
+
+/* Replaces stride::tc_compact (src/kernels_tc.h:85, src/kernels_tc.cu:566-587):
+ * out lane l <- in lane lm_rows[l], for l < lm_count. */
+int stride_tc_compact(const StrideTcCompactParams* p, void* stream);
 
 /* No reference counterpart (a property the reference fixes in code,
  * src/kernels_tc.cu:29-32): the number of K splits used for a weight matrix

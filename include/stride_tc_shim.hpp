@@ -6,8 +6,8 @@
 //     #include "kernels_tc.h"          // stride::TcQkvParams, ... (unchanged)
 //     #include "stride_tc_shim.hpp"    // defines stride::tc_qkv, ... over the C ABI
 //
-// It defines the five functions with the reference signatures
-// (src/kernels_tc.h:81-87). The parameter structs are passed by address: the
+// It defines the nine functions with the reference signatures
+// (src/kernels_tc.h:79-87). The parameter structs are passed by address: the
 // static_asserts below check that the engine's PODs have exactly the layout the
 // C ABI expects. Launches go on stride::tc_stream(), which the engine defines
 // (the counterpart of the reference's kernel_stream(), src/kernels.cu:457-460).
@@ -44,6 +44,10 @@ static_assert(sizeof(BestEntry) == sizeof(StrideBestEntry) && alignof(BestEntry)
 static_assert(offsetof(TcQkvParams, kv) == offsetof(StrideTcQkvParams, kv), "TcQkvParams.kv offset");
 static_assert(offsetof(TcQkvParams, head_dim) == offsetof(StrideTcQkvParams, head_dim), "TcQkvParams.head_dim offset");
 static_assert(offsetof(TcLmGreedyParams, best) == offsetof(StrideTcLmGreedyParams, best), "TcLmGreedyParams.best offset");
+static_assert(offsetof(TcNormParams, eps) == offsetof(StrideTcNormParams, eps), "TcNormParams.eps offset");
+static_assert(offsetof(TcCompactParams, col_tiles) == offsetof(StrideTcCompactParams, col_tiles), "TcCompactParams offset");
+static_assert(offsetof(AttentionParams, kv) == offsetof(StrideAttentionParams, kv), "AttentionParams.kv offset");
+static_assert(offsetof(AttentionParams, scale) == offsetof(StrideAttentionParams, scale), "AttentionParams.scale offset");
 
 }  // namespace tc_shim
 
@@ -68,6 +72,24 @@ void tc_lm_greedy(const TcLmGreedyParams& p, int r, int lt) {
 
 void tc_lm_full(const TcLmFullParams& p, int lt) {
   tc_shim::check(stride_tc_lm_full(tc_shim::as_abi<TcLmFullParams, StrideTcLmFullParams>(p), lt, tc_stream()), "tc_lm_full");
+}
+
+void tc_embed(const TcEmbedParams& p) {
+  tc_shim::check(stride_tc_embed(tc_shim::as_abi<TcEmbedParams, StrideTcEmbedParams>(p), tc_stream()), "tc_embed");
+}
+
+void tc_norm(const TcNormParams& p, bool per_lane) {
+  tc_shim::check(stride_tc_norm(tc_shim::as_abi<TcNormParams, StrideTcNormParams>(p), per_lane ? 1 : 0, tc_stream()),
+                 "tc_norm");
+}
+
+void tc_attention(const AttentionParams& p) {
+  tc_shim::check(stride_tc_attention(tc_shim::as_abi<AttentionParams, StrideAttentionParams>(p), tc_stream()),
+                 "tc_attention");
+}
+
+void tc_compact(const TcCompactParams& p) {
+  tc_shim::check(stride_tc_compact(tc_shim::as_abi<TcCompactParams, StrideTcCompactParams>(p), tc_stream()), "tc_compact");
 }
 
 }  // namespace stride

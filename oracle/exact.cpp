@@ -18,6 +18,9 @@
 //     (src/kernels.cu:407-423, src/kernel_common.h:58-82);
 //   * QKV RoPE: ra = a*c - b*s, rb = b*c + a*s on pairs (d, d + D/2)
 //     (src/kernels.cu:254-267).
+// And the tensor-core path's non-GEMM operators, whose trees differ from the
+// exact path's in places (see the comments at oracle_tc_norm and
+// oracle_tc_attention).
 // Rows are independent, so any split of the work over threads gives the same bits
 // (the fork-join pool of src/cpu_pool.h:24-49 only changes who computes a row).
 //
@@ -242,6 +245,102 @@ int oracle_qkv(const uint16_t* wq, const uint16_t* wk, const uint16_t* wv, int n
       out[static_cast<int64_t>(j) * n + rb_row] = ob;
     }
   });
+  return 0;
+}
+
+// RMSNorm of the tensor-core path (src/kernels_tc.cu:205-271; the per-lane
+// variant :276-340 has the same bits): 32 partials, partial t = fmaf(v, v, acc)
+// over the 16 columns of each column tile ct == t (mod 32), tiles ascending;
+// sum = ((p0 + p1) + ...) + p31; r = 1 / sqrtf(sum / dim + eps);
+// x = bf16(g * (v * r)). (The exact path's RmsNorm, src/kernels.cu:119-200,
+// groups four columns per unit instead of sixteen, so its sum can differ in the
+// last bit.) h and x are row-major [m][dim].
+int oracle_tc_norm(const float* h, int m, int dim, const float* weight, float eps, uint16_t* x) {
+  const int col_tiles = dim / 16;
+  for (int j = 0; j < m; ++j) {
+    const float* v = h + static_cast<int64_t>(j) * dim;
+    float part[32];
+    for (int t = 0; t < 32; ++t) {
+      float acc = 0.0f;
+      for (int ct = t; ct < col_tiles; ct += 32)
+        for (int c = 0; c < 16; ++c) acc = std::fma(v[ct * 16 + c], v[ct * 16 + c], acc);
+      part[t] = acc;
+    }
+    float sum = part[0];
+    for (int t = 1; t < 32; ++t) sum = sum + part[t];
+    const float r = 1.0f / std::sqrt(sum / static_cast<float>(dim) + eps);
+    for (int c = 0; c < dim; ++c) x[static_cast<int64_t>(j) * dim + c] = bf16_rne(weight[c] * (v[c] * r));
+  }
+  return 0;
+}
+
+// Paged attention of the tensor-core path over bf16 KV (src/kernel_common.h:
+// 84-309 with KvT = uint16_t, writer src/kernels_tc.cu:658-666), for groups of
+// four query heads sharing KV group g. For row j, positions 0..row_pos[j] in
+// 64-position pages: per page and head, score_i = (fmaf chain over d ascending
+// of q[d] * k_i[d]) * scale; mp = max score; e_i = det_exp(score_i - mp);
+// den = e_0 + e_1 + ... (left to right); v[d] = fmaf chain over i ascending of
+// e_i * v_i[d]. Then over pages c ascending: M = max mp_c; f_c =
+// det_exp(mp_c - M); D = fmaf chain of f_c * den_c; out[d] = (fmaf chain of
+// f_c * v_c[d]) / D, rounded to bf16. Operands are plain: q [m][n_kv*4][hd] fp32,
+// k and v [slot][g][pos][hd] bf16 bits with `cap` positions per slot,
+// out [m][n_kv*4*hd] bf16 bits.
+int oracle_tc_attention(const float* q, const uint16_t* k, const uint16_t* v, int cap, const int32_t* row_slot,
+                        const int32_t* row_pos, int m, int n_kv, int hd, float scale, uint16_t* out) {
+  const int heads = n_kv * 4;
+  const float neg_inf = f32_of_bits(0xFF800000u);
+  for (int j = 0; j < m; ++j) {
+    const int pages = (row_pos[j] >> 6) + 1;
+    const int visible = row_pos[j] + 1;
+    for (int g = 0; g < n_kv; ++g) {
+      const uint16_t* kg = k + (static_cast<int64_t>(row_slot[j]) * n_kv + g) * cap * hd;
+      const uint16_t* vg = v + (static_cast<int64_t>(row_slot[j]) * n_kv + g) * cap * hd;
+      std::vector<float> mp(static_cast<size_t>(pages) * 4), den(static_cast<size_t>(pages) * 4),
+          vs(static_cast<size_t>(pages) * 4 * hd);
+      for (int c = 0; c < pages; ++c) {
+        const int p0 = c * 64;
+        const int n = visible - p0 < 64 ? visible - p0 : 64;
+        for (int h = 0; h < 4; ++h) {
+          const float* qh = q + (static_cast<int64_t>(j) * heads + g * 4 + h) * hd;
+          float sc[64];
+          float mx = neg_inf;
+          for (int i = 0; i < n; ++i) {
+            float a = 0.0f;
+            for (int d = 0; d < hd; ++d) a = std::fma(qh[d], widen_bf16(kg[static_cast<int64_t>(p0 + i) * hd + d]), a);
+            sc[i] = a * scale;
+            if (sc[i] > mx) mx = sc[i];
+          }
+          float e[64];
+          for (int i = 0; i < n; ++i) e[i] = det_exp(sc[i] - mx);
+          float dn = 0.0f;
+          for (int i = 0; i < n; ++i) dn = dn + e[i];
+          mp[c * 4 + h] = mx;
+          den[c * 4 + h] = dn;
+          for (int d = 0; d < hd; ++d) {
+            float a = 0.0f;
+            for (int i = 0; i < n; ++i) a = std::fma(e[i], widen_bf16(vg[static_cast<int64_t>(p0 + i) * hd + d]), a);
+            vs[(static_cast<size_t>(c) * 4 + h) * hd + d] = a;
+          }
+        }
+      }
+      for (int h = 0; h < 4; ++h) {
+        float M = neg_inf;
+        for (int c = 0; c < pages; ++c)
+          if (mp[c * 4 + h] > M) M = mp[c * 4 + h];
+        std::vector<float> f(pages);
+        float dn = 0.0f;
+        for (int c = 0; c < pages; ++c) {
+          f[c] = det_exp(mp[c * 4 + h] - M);
+          dn = std::fma(f[c], den[c * 4 + h], dn);
+        }
+        for (int d = 0; d < hd; ++d) {
+          float acc = 0.0f;
+          for (int c = 0; c < pages; ++c) acc = std::fma(f[c], vs[(static_cast<size_t>(c) * 4 + h) * hd + d], acc);
+          out[static_cast<int64_t>(j) * heads * hd + (g * 4 + h) * hd + d] = bf16_rne(acc / dn);
+        }
+      }
+    }
+  }
   return 0;
 }
 

@@ -152,6 +152,31 @@ class Exact(_Base):
     def bf16_rne(self, v: float) -> int:
         return self.lib.oracle_bf16_rne(v)
 
+    def tc_norm(self, h, weight, eps: float):
+        """Tensor-core-path RMSNorm of rows h [m][dim] -> bf16 bits [m][dim]."""
+        h, weight = _f32(h), _f32(weight)
+        m, dim = h.shape
+        x = np.zeros((m, dim), np.uint16)
+        f = self.lib.oracle_tc_norm
+        f.argtypes = [_f32p, C.c_int, C.c_int, _f32p, C.c_float, _u16p]
+        if f(h, m, dim, weight, eps, x) != 0:
+            raise ValueError("oracle_tc_norm rejected its arguments")
+        return x
+
+    def tc_attention(self, q, k, v, row_slot, row_pos, scale: float):
+        """Tensor-core-path attention. q [m][n_kv*4][hd] fp32; k, v [slots][n_kv][cap][hd]
+        bf16 bits -> out bf16 bits [m][n_kv*4*hd]."""
+        q, k, v = _f32(q), _u16(k), _u16(v)
+        m, heads, hd = q.shape
+        n_kv, cap = k.shape[1], k.shape[2]
+        out = np.zeros((m, heads * hd), np.uint16)
+        f = self.lib.oracle_tc_attention
+        f.argtypes = [_f32p, _u16p, _u16p, C.c_int, _i32p, _i32p, C.c_int, C.c_int, C.c_int, C.c_float, _u16p]
+        if f(q, k, v, cap, np.ascontiguousarray(row_slot, dtype=np.int32), np.ascontiguousarray(row_pos, dtype=np.int32),
+             m, n_kv, hd, scale, out) != 0:
+            raise ValueError("oracle_tc_attention rejected its arguments")
+        return out
+
 
 class Ref(_Base):
     """The reference's own exact path (oracle/_ref/libstride_ref.so)."""
@@ -170,6 +195,40 @@ class Ref(_Base):
         z = np.zeros((m, n), np.float32)
         self._call("mlp13", w1, w3, n, k, x, m, z)
         return z
+
+    def embed(self, emb, tokens):
+        """Exact-path embedding of bf16 rows emb [vocab][dim] -> fp32 [m][dim]."""
+        emb = _u16(emb)
+        vocab, dim = emb.shape
+        tokens = np.ascontiguousarray(tokens, dtype=np.int32)
+        h = np.zeros((tokens.size, dim), np.float32)
+        f = self.lib.ref_embed
+        f.argtypes = [_u16p, C.c_int, C.c_int, _i32p, C.c_int, _f32p]
+        self._call("embed", emb, vocab, dim, tokens, tokens.size, h)
+        return h
+
+    def norm(self, h, weight, eps: float):
+        """Exact-path RMSNorm of rows h [m][dim] -> fp32 [m][dim]."""
+        h, weight = _f32(h), _f32(weight)
+        m, dim = h.shape
+        out = np.zeros((m, dim), np.float32)
+        f = self.lib.ref_norm
+        f.argtypes = [_f32p, C.c_int, C.c_int, _f32p, C.c_float, _f32p]
+        self._call("norm", h, m, dim, weight, eps, out)
+        return out
+
+    def attention(self, q, k, v, row_slot, row_pos, scale: float):
+        """Exact-path attention over fp32 KV holding the widened bf16 k, v
+        [slots][n_kv][cap][hd] -> fp32 [m][n_kv*4*hd]."""
+        q, k, v = _f32(q), _u16(k), _u16(v)
+        m, heads, hd = q.shape
+        slots, n_kv, cap = k.shape[0], k.shape[1], k.shape[2]
+        out = np.zeros((m, heads * hd), np.float32)
+        f = self.lib.ref_attention
+        f.argtypes = [_f32p, _u16p, _u16p, C.c_int, C.c_int, _i32p, _i32p, C.c_int, C.c_int, C.c_int, C.c_float, _f32p]
+        self._call("attention", q, k, v, slots, cap, np.ascontiguousarray(row_slot, dtype=np.int32),
+                   np.ascontiguousarray(row_pos, dtype=np.int32), m, n_kv, hd, scale, out)
+        return out
 
 
 def ref_available() -> bool:

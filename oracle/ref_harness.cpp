@@ -8,8 +8,8 @@
 //   RoPE rows (d0, d0+1, d0+D/2, d0+D/2+1)   (rope_rows, src/model.cpp:170-176)
 //   activations dim-major A[dim*stride+lane] (src/kernels.h:3-8, lane_shape
 //                                             src/engine.cpp:24-28)
-// and calls k_lm_full / k_gemm_residual / k_mlp13 / k_lm_greedy / k_qkv
-// (src/kernels.h:236-244). Signatures mirror oracle/exact.cpp so the two can be
+// and calls k_lm_full / k_gemm_residual / k_mlp13 / k_lm_greedy / k_qkv, and
+// k_embed / k_norm / k_attention for the non-GEMM operators (src/kernels.h:236-244). Signatures mirror oracle/exact.cpp so the two can be
 // compared element for element.
 #include <cstdint>
 #include <cstring>
@@ -210,6 +210,105 @@ int ref_qkv(const uint16_t* wq, const uint16_t* wk, const uint16_t* wv, int nq, 
         v_out[static_cast<size_t>(j) * nkv + hd * D + d] = arena[base + kv.which_elems];
       }
   }
+  return 0;
+}
+
+
+// Exact-path embedding (src/kernels.cu:98-117) of plain bf16 rows emb[vocab][dim]
+// (packed into the exact path's [vocab/4][dim][4] layout) into h[m][dim].
+int ref_embed(const uint16_t* emb, int vocab, int dim, const int32_t* tokens, int m, float* h) {
+  const int groups = (vocab + 3) / 4;
+  const Shape s = lane_shape(m);
+  std::vector<uint16_t> ep = pack4(emb, vocab, dim, groups, plain_rows(groups));
+  std::vector<float> hd(static_cast<size_t>(dim) * s.stride + 16, 0.0f);
+  EmbedParams p{};
+  p.l = lanes_of(m, s);
+  p.embed = ep.data();
+  p.tokens = tokens;
+  p.h = hd.data();
+  p.dim = dim;
+  k_embed(p);
+  for (int j = 0; j < m; ++j)
+    for (int c = 0; c < dim; ++c) h[static_cast<size_t>(j) * dim + c] = hd[static_cast<size_t>(c) * s.stride + j];
+  return 0;
+}
+
+// Exact-path RMSNorm (src/kernels.cu:119-200), fp32 out[m][dim].
+int ref_norm(const float* h, int m, int dim, const float* weight, float eps, float* out) {
+  const Shape s = lane_shape(m);
+  std::vector<float> hd = dim_major(h, m, dim, s);
+  std::vector<float> od(hd.size(), 0.0f);
+  NormParams p{};
+  p.l = lanes_of(m, s);
+  p.in = hd.data();
+  p.out = od.data();
+  p.weight = weight;
+  p.dim = dim;
+  p.eps = eps;
+  k_norm(p, s.J);
+  for (int j = 0; j < m; ++j)
+    for (int c = 0; c < dim; ++c) out[static_cast<size_t>(j) * dim + c] = od[static_cast<size_t>(c) * s.stride + j];
+  return 0;
+}
+
+// Exact-path attention (src/kernels.cu:474-485, src/kernel_common.h:84-309) over
+// fp32 KV holding the widened bf16 values k, v [slot][g][pos][hd] (cap positions
+// per slot), laid out in the reference's 64-token KV blocks; fp32 out[m][heads*hd].
+int ref_attention(const float* q, const uint16_t* k, const uint16_t* v, int slots, int cap, const int32_t* row_slot,
+                  const int32_t* row_pos, int m, int n_kv, int hd, float scale, float* out) {
+  const Shape s = lane_shape(m);
+  const int heads = n_kv * 4;
+  const int max_blocks = (cap + kKvBlockTokens - 1) / kKvBlockTokens;
+  const int64_t group_elems = static_cast<int64_t>(kKvBlockTokens) * hd;
+  const int64_t which_elems = n_kv * group_elems;
+  const int64_t block_elems = 2 * which_elems;
+  std::vector<float> arena(static_cast<size_t>(slots) * max_blocks * block_elems, 0.0f);
+  std::vector<int32_t> table(static_cast<size_t>(slots) * max_blocks);
+  for (int sl = 0; sl < slots; ++sl)
+    for (int b = 0; b < max_blocks; ++b) table[static_cast<size_t>(sl) * max_blocks + b] = sl * max_blocks + b;
+  for (int sl = 0; sl < slots; ++sl)
+    for (int g = 0; g < n_kv; ++g)
+      for (int pos = 0; pos < cap; ++pos)
+        for (int which = 0; which < 2; ++which) {
+          const uint16_t* src = (which ? v : k) + ((static_cast<int64_t>(sl) * n_kv + g) * cap + pos) * hd;
+          float* dst = arena.data() + (static_cast<int64_t>(sl) * max_blocks + pos / kKvBlockTokens) * block_elems +
+                       which * which_elems + g * group_elems + static_cast<int64_t>(pos % kKvBlockTokens) * hd;
+          for (int d = 0; d < hd; ++d) {
+            const uint32_t bits = static_cast<uint32_t>(src[d]) << 16;
+            std::memcpy(&dst[d], &bits, 4);
+          }
+        }
+  std::vector<int32_t> items;
+  for (int j = 0; j < m; ++j)
+    for (int page = 0; page <= (row_pos[j] >> kKvBlockShift); ++page) {
+      items.push_back(j);
+      items.push_back(page);
+    }
+  const int rec_floats = 4 * hd + 8;
+  std::vector<float> scratch(static_cast<size_t>(m) * n_kv * max_blocks * rec_floats, 0.0f);
+  std::vector<float> od(static_cast<size_t>(heads) * hd * s.stride + 16, 0.0f);
+  AttentionParams p{};
+  p.l = lanes_of(m, s);
+  p.q = q;
+  p.q_stride = heads * hd;
+  p.out = od.data();
+  p.out_cols = heads * hd;
+  p.kv = KvRef{arena.data(), table.data(), block_elems, block_elems, which_elems, group_elems, max_blocks, hd};
+  p.row_slot = row_slot;
+  p.row_pos = row_pos;
+  p.items = items.data();
+  p.item_count = static_cast<int32_t>(items.size() / 2);
+  p.scratch = scratch.data();
+  p.max_pages = max_blocks;
+  p.rec_floats = rec_floats;
+  p.layer = 0;
+  p.n_kv = n_kv;
+  p.n_q = 4;
+  p.head_dim = hd;
+  p.scale = scale;
+  k_attention(p);
+  for (int j = 0; j < m; ++j)
+    for (int c = 0; c < heads * hd; ++c) out[static_cast<size_t>(j) * heads * hd + c] = od[static_cast<size_t>(c) * s.stride + j];
   return 0;
 }
 

@@ -75,6 +75,43 @@ class TcLmFullParams(C.Structure):  # src/kernels_tc.h:72-77
     _fields_ = [("l", Lanes), ("x", C.c_void_p), ("m", GemmMat), ("logits", C.c_void_p)]
 
 
+class TcEmbedParams(C.Structure):  # src/kernels_tc.h:10-16
+    _fields_ = [("l", Lanes), ("embed", C.c_void_p), ("tokens", C.c_void_p), ("h", C.c_void_p), ("dim", C.c_int32)]
+
+
+class TcNormParams(C.Structure):  # src/kernels_tc.h:18-25
+    _fields_ = [("l", Lanes), ("h", C.c_void_p), ("x", C.c_void_p), ("weight", C.c_void_p), ("dim", C.c_int32),
+                ("eps", C.c_float)]
+
+
+class TcCompactParams(C.Structure):  # src/kernels_tc.h:55-62
+    _fields_ = [("l", Lanes), ("in_", C.c_void_p), ("out", C.c_void_p), ("lm_rows", C.c_void_p),
+                ("lm_count", C.c_int32), ("col_tiles", C.c_int32)]
+
+
+class AttentionParams(C.Structure):  # src/kernels.h:79-98
+    _fields_ = [
+        ("l", Lanes),
+        ("q", C.c_void_p),
+        ("q_stride", C.c_int32),
+        ("out", C.c_void_p),
+        ("out_cols", C.c_int32),
+        ("kv", KvRef),
+        ("row_slot", C.c_void_p),
+        ("row_pos", C.c_void_p),
+        ("items", C.c_void_p),
+        ("item_count", C.c_int32),
+        ("scratch", C.c_void_p),
+        ("max_pages", C.c_int32),
+        ("rec_floats", C.c_int32),
+        ("layer", C.c_int32),
+        ("n_kv", C.c_int32),
+        ("n_q", C.c_int32),
+        ("head_dim", C.c_int32),
+        ("scale", C.c_float),
+    ]
+
+
 # Symbols the library must export (everything include/stride_tc.h declares).
 EXPORTS = (
     "stride_tc_qkv",
@@ -82,6 +119,10 @@ EXPORTS = (
     "stride_tc_mlp13",
     "stride_tc_lm_greedy",
     "stride_tc_lm_full",
+    "stride_tc_embed",
+    "stride_tc_norm",
+    "stride_tc_attention",
+    "stride_tc_compact",
     "stride_tc_split_count",
     "stride_tc_last_error",
     "stride_tc_version",
@@ -104,6 +145,8 @@ def check_layout() -> None:
     assert C.sizeof(TcMlp13Params) == 64
     assert C.sizeof(TcLmGreedyParams) == 56
     assert C.sizeof(TcLmFullParams) == 48
+    assert C.sizeof(TcEmbedParams) == 48 and C.sizeof(TcNormParams) == 48 and C.sizeof(TcCompactParams) == 48
+    assert AttentionParams.kv.offset == 48 and C.sizeof(AttentionParams) == 176
 
 
 class StrideTcError(RuntimeError):
@@ -131,8 +174,13 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     lib.stride_tc_mlp13.argtypes = [C.POINTER(TcMlp13Params), C.c_int, C.c_int, vp]
     lib.stride_tc_lm_greedy.argtypes = [C.POINTER(TcLmGreedyParams), C.c_int, C.c_int, vp]
     lib.stride_tc_lm_full.argtypes = [C.POINTER(TcLmFullParams), C.c_int, vp]
+    lib.stride_tc_embed.argtypes = [C.POINTER(TcEmbedParams), vp]
+    lib.stride_tc_norm.argtypes = [C.POINTER(TcNormParams), C.c_int, vp]
+    lib.stride_tc_attention.argtypes = [C.POINTER(AttentionParams), vp]
+    lib.stride_tc_compact.argtypes = [C.POINTER(TcCompactParams), vp]
     for name in ("stride_tc_qkv", "stride_tc_gemm_residual", "stride_tc_mlp13", "stride_tc_lm_greedy",
-                 "stride_tc_lm_full", "stride_tc_split_count"):
+                 "stride_tc_lm_full", "stride_tc_embed", "stride_tc_norm", "stride_tc_attention", "stride_tc_compact",
+                 "stride_tc_split_count"):
         getattr(lib, name).restype = C.c_int
     lib.stride_tc_split_count.argtypes = [C.c_int32, C.c_int32]
     lib.stride_tc_set_stream_config.argtypes = [C.c_int32]

@@ -11,7 +11,7 @@ import subprocess
 import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-SOURCES = [os.path.join(HERE, "csrc", "tc_gemm.hip")]
+SOURCES = [os.path.join(HERE, "csrc", "tc_gemm.hip"), os.path.join(HERE, "csrc", "tc_aux.hip")]
 OUT = os.path.join(HERE, "libstride_tc.so")
 PROBE_SOURCES = [os.path.join(HERE, "csrc", "probe.hip")]
 PROBE_OUT = os.path.join(HERE, "libstride_probe.so")

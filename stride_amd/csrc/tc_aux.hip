@@ -1,0 +1,345 @@
+// The non-GEMM entry points of stride's tensor-core path for MI355X (gfx950):
+// token embedding into fp32 h tiles, RMSNorm from h to bf16 x tiles, paged
+// attention over bf16 KV, and lane compaction. They complete the operator
+// surface of the reference's src/kernels_tc.h:79-87, so an engine linking this
+// library needs no other device code for a decode step.
+//
+// Each follows the reference's fixed summation trees exactly (the order of every
+// fmaf and add, src/kernels_tc.cu:179-340, src/kernel_common.h:84-309), so the
+// results do not depend on the batch, the lane position or the launch shape.
+// Work is spread over 64-wide wavefronts wherever the tree leaves freedom
+// (independent positions, dimensions and lanes); sequential sums stay sequential.
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <string>
+
+#include "tc_common.hpp"
+
+namespace stride_tc {
+
+int fail(int code, const std::string& msg);  // tc_gemm.hip
+
+namespace {
+
+// Attention summation page: 64 positions (src/kernels.h:20-21). A numeric
+// constant of the tree, independent of the KV storage page size.
+constexpr int kAttnPageShift = 6;
+constexpr int kAttnPage = 1 << kAttnPageShift;
+constexpr int kMaxHeadDim = 128;
+constexpr int kHeadsPerGroup = 4;  // the reference's float4 query packing
+
+// ---------------------------------------------------------------------------
+// Embedding: lane j of the h tiles <- fp32(embed row tokens[j]). The embedding
+// is the LM head's weight tiles, so row `token` is slot token % 16 of row tile
+// token / 16 (src/kernels_tc.cu:179-203). Thread i moves 8 columns.
+__global__ __launch_bounds__(256) void k_embed(StrideTcEmbedParams p) {
+  const int b = blockIdx.x;
+  const int token = p.tokens[b];
+  const int rt = token >> 4, slot = token & 15, lt = b >> 4, jj = b & 15;
+  const int col_tiles = p.dim >> 4;
+  for (int i = threadIdx.x; i < col_tiles * 2; i += blockDim.x) {
+    const int ct = i >> 1, half = i & 1;
+    const uint16_t* src = p.embed + (static_cast<int64_t>(rt) * col_tiles + ct) * kTileElems + slot * 16 + half * 8;
+    float* dst = p.h + ((static_cast<int64_t>(lt) * col_tiles + ct) * 16 + jj) * 16 + half * 8;
+    const u32x4 w = load16(src);
+    f32x4 lo, hi;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      lo[2 * k] = f32_of(w[k] << 16);
+      lo[2 * k + 1] = f32_of(w[k] & 0xFFFF0000u);
+      hi[2 * k] = f32_of(w[k + 2] << 16);
+      hi[2 * k + 1] = f32_of(w[k + 2] & 0xFFFF0000u);
+    }
+    reinterpret_cast<f32x4*>(dst)[0] = lo;
+    reinterpret_cast<f32x4*>(dst)[1] = hi;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// RMSNorm, one wave per lane. Lanes 0..31 of the wave compute the reference's
+// 32 partials (partial t: fmaf over columns 0..15 of column tiles ct == t mod
+// 32, ascending); lane 0 adds them left to right; every lane then writes its
+// column tiles as bf16(g * (v * r)) (src/kernels_tc.cu:205-271, 276-340).
+__global__ __launch_bounds__(64) void k_norm(StrideTcNormParams p, int per_lane) {
+  const int b = blockIdx.x;  // lane index in [0, lane_groups * 16)
+  const int lane = threadIdx.x;
+  const int lt = b >> 4, j = b & 15;
+  const int col_tiles = p.dim >> 4;
+  const int64_t row0 = static_cast<int64_t>(lt) * col_tiles * kTileElems + j * 16;
+  if (b >= p.l.rows) {
+    if (per_lane) return;
+    for (int ct = lane; ct < col_tiles; ct += 64) {
+      u32x4* out = reinterpret_cast<u32x4*>(p.x + row0 + static_cast<int64_t>(ct) * kTileElems);
+      out[0] = u32x4{0u, 0u, 0u, 0u};
+      out[1] = u32x4{0u, 0u, 0u, 0u};
+    }
+    return;
+  }
+  __shared__ float partial[32];
+  __shared__ float rs;
+  if (lane < 32) {
+    float acc = 0.0f;
+    for (int ct = lane; ct < col_tiles; ct += 32) {
+      const f32x4* v = reinterpret_cast<const f32x4*>(p.h + row0 + static_cast<int64_t>(ct) * kTileElems);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const f32x4 w = v[q];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc = __builtin_fmaf(w[c], w[c], acc);
+      }
+    }
+    partial[lane] = acc;
+  }
+  __syncthreads();
+  if (lane == 0) {
+    float sum = partial[0];
+    for (int i = 1; i < 32; ++i) sum = sum + partial[i];
+    rs = 1.0f / sqrtf(sum / static_cast<float>(p.dim) + p.eps);
+  }
+  __syncthreads();
+  const float r = rs;
+  for (int ct = lane; ct < col_tiles; ct += 64) {
+    const f32x4* v = reinterpret_cast<const f32x4*>(p.h + row0 + static_cast<int64_t>(ct) * kTileElems);
+    const f32x4* gv = reinterpret_cast<const f32x4*>(p.weight + ct * 16);
+    uint32_t o[8];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const f32x4 w = v[q], g = gv[q];
+      const uint32_t b0 = bf16_rne(g[0] * (w[0] * r)), b1 = bf16_rne(g[1] * (w[1] * r));
+      const uint32_t b2 = bf16_rne(g[2] * (w[2] * r)), b3 = bf16_rne(g[3] * (w[3] * r));
+      o[2 * q] = b0 | (b1 << 16);
+      o[2 * q + 1] = b2 | (b3 << 16);
+    }
+    u32x4* out = reinterpret_cast<u32x4*>(p.x + row0 + static_cast<int64_t>(ct) * kTileElems);
+    out[0] = u32x4{o[0], o[1], o[2], o[3]};
+    out[1] = u32x4{o[4], o[5], o[6], o[7]};
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Lane compaction: out lane l <- in lane lm_rows[l] (src/kernels_tc.cu:566-587).
+__global__ __launch_bounds__(64) void k_compact(StrideTcCompactParams p) {
+  const int b = blockIdx.x;
+  const int src = p.lm_rows[b];
+  const int64_t in0 = static_cast<int64_t>(src >> 4) * p.col_tiles * kTileElems + (src & 15) * 16;
+  const int64_t out0 = static_cast<int64_t>(b >> 4) * p.col_tiles * kTileElems + (b & 15) * 16;
+  for (int ct = threadIdx.x; ct < p.col_tiles; ct += 64) {
+    const u32x4* in = reinterpret_cast<const u32x4*>(p.in + in0 + static_cast<int64_t>(ct) * kTileElems);
+    u32x4* out = reinterpret_cast<u32x4*>(p.out + out0 + static_cast<int64_t>(ct) * kTileElems);
+    out[0] = in[0];
+    out[1] = in[1];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Attention.
+
+// K or V row of position pos for KV group `group` (src/kernel_common.h:20-25),
+// with the storage page given by the arena geometry.
+__device__ __forceinline__ const uint16_t* kv_row(const StrideKvRef& kv, int page_shift, int layer, int which, int group,
+                                                  int slot, int pos) {
+  const int64_t block = kv.table[static_cast<int64_t>(slot) * kv.max_blocks + (pos >> page_shift)];
+  const int token = pos & ((1 << page_shift) - 1);
+  return static_cast<const uint16_t*>(kv.arena) + block * kv.block_elems + layer * kv.layer_elems +
+         which * kv.which_elems + group * kv.group_elems + static_cast<int64_t>(token) * kv.head_dim;
+}
+
+__device__ __forceinline__ float bf16_at(const uint16_t* row, int d) { return f32_of(static_cast<uint32_t>(row[d]) << 16); }
+
+// One (row, page) item for one KV group (src/kernel_common.h:84-250). Lane i
+// scores position p0 + i for the four query heads (an fmaf chain over the head
+// dims in order, then times scale); the page maximum is order-free; the
+// exponentials follow; lanes 0..3 add one head's weights left to right; each
+// lane then mixes the values of its dims over the positions in order.
+__global__ __launch_bounds__(64) void k_attn_page(StrideAttentionParams p, int page_shift) {
+  const int item = blockIdx.x / p.n_kv;
+  const int g = blockIdx.x % p.n_kv;
+  const int lane = threadIdx.x;
+  const int j = p.items[2 * item];
+  const int page = p.items[2 * item + 1];
+  const int slot = p.row_slot[j];
+  const int visible = p.row_pos[j] + 1;
+  const int p0 = page << kAttnPageShift;
+  const int n = min(visible - p0, kAttnPage);
+  const int D = p.head_dim;
+  __shared__ float q[kHeadsPerGroup][kMaxHeadDim];
+  __shared__ float w[kHeadsPerGroup][kAttnPage];
+  __shared__ float mm[kHeadsPerGroup], den[kHeadsPerGroup];
+
+  const float* qrow = p.q + static_cast<int64_t>(j) * p.q_stride + static_cast<int64_t>(g * kHeadsPerGroup) * D;
+  for (int i = lane; i < kHeadsPerGroup * D; i += 64) q[i / D][i % D] = qrow[i];
+  __syncthreads();
+
+  const float neg_inf = f32_of(0xFF800000u);
+  float sc[kHeadsPerGroup];
+#pragma unroll
+  for (int h = 0; h < kHeadsPerGroup; ++h) sc[h] = neg_inf;
+  if (lane < n) {
+    const uint16_t* key = kv_row(p.kv, page_shift, p.layer, 0, g, slot, p0 + lane);
+    float a[kHeadsPerGroup] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int d = 0; d < D; d += 8) {
+      const u32x4 kw = load16(key + d);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float k = f32_of(e & 1 ? kw[e >> 1] & 0xFFFF0000u : kw[e >> 1] << 16);
+#pragma unroll
+        for (int h = 0; h < kHeadsPerGroup; ++h) a[h] = __builtin_fmaf(q[h][d + e], k, a[h]);
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < kHeadsPerGroup; ++h) sc[h] = a[h] * p.scale;
+  }
+  // Page maximum (a max is independent of the order it is taken in).
+#pragma unroll
+  for (int h = 0; h < kHeadsPerGroup; ++h) {
+    float m = sc[h];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      const float o = __shfl_xor(m, off);
+      if (o > m) m = o;
+    }
+    if (lane < n) w[h][lane] = det_exp(sc[h] - m);
+    if (lane == 0) mm[h] = m;
+  }
+  __syncthreads();
+  if (lane < kHeadsPerGroup) {
+    float s = 0.0f;
+    for (int i = 0; i < n; ++i) s = s + w[lane][i];
+    den[lane] = s;
+  }
+  __syncthreads();
+  float* rec = p.scratch + (static_cast<int64_t>(j * p.n_kv + g) * p.max_pages + page) * p.rec_floats;
+  if (lane < kHeadsPerGroup) {
+    rec[lane] = mm[lane];
+    rec[4 + lane] = den[lane];
+  }
+  float* v_out = rec + 8;
+  for (int d = lane; d < D; d += 64) {
+    float a[kHeadsPerGroup] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int i = 0; i < n; ++i) {
+      const float v = bf16_at(kv_row(p.kv, page_shift, p.layer, 1, g, slot, p0 + i), d);
+#pragma unroll
+      for (int h = 0; h < kHeadsPerGroup; ++h) a[h] = __builtin_fmaf(w[h][i], v, a[h]);
+    }
+#pragma unroll
+    for (int h = 0; h < kHeadsPerGroup; ++h) v_out[h * D + d] = a[h];
+  }
+}
+
+// Ascending-page combine of one row's records for one KV group, written as bf16
+// x tiles (src/kernel_common.h:252-309, writer src/kernels_tc.cu:658-666).
+__global__ __launch_bounds__(64) void k_attn_combine(StrideAttentionParams p) {
+  extern __shared__ float f[];  // [4][max_pages]
+  __shared__ float den[kHeadsPerGroup];
+  const int j = blockIdx.x / p.n_kv;
+  const int g = blockIdx.x % p.n_kv;
+  const int lane = threadIdx.x;
+  const int pages = (p.row_pos[j] >> kAttnPageShift) + 1;
+  const int D = p.head_dim;
+  const float* recs = p.scratch + static_cast<int64_t>(j * p.n_kv + g) * p.max_pages * p.rec_floats;
+  if (lane < kHeadsPerGroup) {
+    float m = f32_of(0xFF800000u);
+    for (int c = 0; c < pages; ++c) {
+      const float mc = recs[static_cast<int64_t>(c) * p.rec_floats + lane];
+      if (mc > m) m = mc;
+    }
+    float d = 0.0f;
+    for (int c = 0; c < pages; ++c) {
+      const float* rec = recs + static_cast<int64_t>(c) * p.rec_floats;
+      const float e = det_exp(rec[lane] - m);
+      f[lane * p.max_pages + c] = e;
+      d = __builtin_fmaf(e, rec[4 + lane], d);
+    }
+    den[lane] = d;
+  }
+  __syncthreads();
+  const int col_tiles = p.out_cols >> 4;
+  uint16_t* out = static_cast<uint16_t*>(p.out);
+  const int64_t lane0 = static_cast<int64_t>(j >> 4) * col_tiles * kTileElems + (j & 15) * 16;
+  for (int d = lane; d < D; d += 64) {
+    for (int qh = 0; qh < p.n_q; ++qh) {
+      float acc = 0.0f;
+      for (int c = 0; c < pages; ++c)
+        acc = __builtin_fmaf(f[qh * p.max_pages + c], recs[static_cast<int64_t>(c) * p.rec_floats + 8 + qh * D + d], acc);
+      const int idx = (g * p.n_q + qh) * D + d;
+      out[lane0 + static_cast<int64_t>(idx >> 4) * kTileElems + (idx & 15)] = static_cast<uint16_t>(bf16_rne(acc / den[qh]));
+    }
+  }
+}
+
+bool lanes_valid(const StrideLanes& l) { return l.rows >= 0 && l.lane_groups == (l.rows + 15) / 16; }
+
+}  // namespace
+}  // namespace stride_tc
+
+using namespace stride_tc;
+
+static_assert(sizeof(StrideTcEmbedParams) == 48, "TcEmbedParams layout");
+static_assert(sizeof(StrideTcNormParams) == 48, "TcNormParams layout");
+static_assert(sizeof(StrideTcCompactParams) == 48, "TcCompactParams layout");
+static_assert(offsetof(StrideAttentionParams, kv) == 48 && sizeof(StrideAttentionParams) == 176,
+              "AttentionParams layout");
+
+static int launched(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(static_cast<int>(e), std::string(what) + " launch failed: " + hipGetErrorString(e));
+  return 0;
+}
+
+extern "C" {
+
+int stride_tc_embed(const StrideTcEmbedParams* p, void* stream) {
+  if (!p || !lanes_valid(p->l) || p->dim <= 0 || p->dim % 16 != 0 || (p->l.rows > 0 && (!p->embed || !p->tokens || !p->h)))
+    return fail(STRIDE_TC_EINVAL, "tc_embed: need rows >= 0, lane_groups = ceil(rows/16), dim a positive multiple of 16 and pointers");
+  if (p->l.rows == 0) return 0;
+  hipLaunchKernelGGL(k_embed, dim3(p->l.rows), dim3(256), 0, static_cast<hipStream_t>(stream), *p);
+  return launched("tc_embed");
+}
+
+int stride_tc_norm(const StrideTcNormParams* p, int per_lane, void* stream) {
+  if (!p || !lanes_valid(p->l) || p->dim <= 0 || p->dim % 16 != 0 ||
+      (p->l.rows > 0 && (!p->h || !p->x || !p->weight)))
+    return fail(STRIDE_TC_EINVAL, "tc_norm: need rows >= 0, lane_groups = ceil(rows/16), dim a positive multiple of 16 and pointers");
+  if (p->l.rows == 0) return 0;
+  hipLaunchKernelGGL(k_norm, dim3(p->l.lane_groups * 16), dim3(64), 0, static_cast<hipStream_t>(stream), *p, per_lane ? 1 : 0);
+  return launched("tc_norm");
+}
+
+int stride_tc_compact(const StrideTcCompactParams* p, void* stream) {
+  if (!p || p->lm_count < 0 || p->col_tiles <= 0 || (p->lm_count > 0 && (!p->in || !p->out || !p->lm_rows)))
+    return fail(STRIDE_TC_EINVAL, "tc_compact: need lm_count >= 0, col_tiles > 0 and pointers");
+  if (p->lm_count == 0) return 0;
+  hipLaunchKernelGGL(k_compact, dim3(p->lm_count), dim3(64), 0, static_cast<hipStream_t>(stream), *p);
+  return launched("tc_compact");
+}
+
+int stride_tc_attention(const StrideAttentionParams* p, void* stream) {
+  if (!p) return fail(STRIDE_TC_EINVAL, "tc_attention: null parameters");
+  const int D = p->head_dim;
+  const int64_t page_tokens = D > 0 ? p->kv.group_elems / D : 0;
+  int page_shift = 0;
+  while (page_shift < 30 && (int64_t{1} << page_shift) < page_tokens) ++page_shift;
+  std::string why;
+  if (!lanes_valid(p->l)) why = "lane_groups must equal ceil(rows/16)";
+  else if (D <= 0 || D > kMaxHeadDim || D % 16 != 0 || p->kv.head_dim != D) why = "head_dim must be a multiple of 16 up to 128 and match kv.head_dim";
+  else if (p->n_q != kHeadsPerGroup) why = "four query heads per KV group are required (the reference packs them in a float4)";
+  else if (p->n_kv <= 0 || p->rec_floats < 8 + 4 * D || p->max_pages <= 0 || p->item_count < 0) why = "bad n_kv, rec_floats, max_pages or item_count";
+  else if (page_tokens <= 0 || (int64_t{1} << page_shift) != page_tokens) why = "the KV storage page (group_elems / head_dim) must be a power of two";
+  else if (p->out_cols % 16 != 0 || p->out_cols < p->n_kv * p->n_q * D) why = "out_cols must be a multiple of 16 covering every head";
+  else if (p->l.rows > 0 && (!p->q || !p->out || !p->kv.arena || !p->kv.table || !p->row_slot || !p->row_pos || !p->scratch ||
+                             (p->item_count > 0 && !p->items)))
+    why = "missing pointer";
+  else if (static_cast<size_t>(p->max_pages) * 4 * sizeof(float) > 64 * 1024) why = "max_pages too large for the combine's LDS";
+  if (!why.empty()) return fail(STRIDE_TC_EINVAL, "tc_attention: " + why);
+  if (p->l.rows == 0) return 0;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (p->item_count > 0) {
+    hipLaunchKernelGGL(k_attn_page, dim3(p->item_count * p->n_kv), dim3(64), 0, st, *p, page_shift);
+    if (int rc = launched("tc_attention (pages)")) return rc;
+  }
+  hipLaunchKernelGGL(k_attn_combine, dim3(p->l.rows * p->n_kv), dim3(64), p->max_pages * 4 * sizeof(float), st, *p);
+  return launched("tc_attention (combine)");
+}
+
+}  // extern "C"

@@ -107,6 +107,84 @@ class PagedKv:
         return torch.stack(rows)
 
 
+    def fill_dense(self, layer: int, which: int, dense) -> None:
+        """Write dense bf16 bits [slots][kv_heads][cap][head_dim] (cap <= pages * page
+        tokens) into the arena through the page table."""
+        slots, kvh, cap, hd = dense.shape
+        r = self.ref
+        dev = self.arena.device
+        pos = torch.arange(cap, device=dev)
+        blk = self.table.long()[:, (pos // self.page_tokens)]                       # [slots][cap]
+        base = blk * r.block_elems + layer * r.layer_elems + which * r.which_elems + (pos % self.page_tokens) * hd
+        idx = (base[:, None, :, None] + torch.arange(kvh, device=dev)[None, :, None, None] * r.group_elems
+               + torch.arange(hd, device=dev)[None, None, None, :])
+        self.arena[idx.reshape(-1)] = dense.reshape(-1).to(dev)
+
+
+def embed(emb_tiles, tokens, rows: int, dim: int, h_out=None):
+    """tc_embed: lane j of fp32 h tiles <- embedding row tokens[j]."""
+    lt = (rows + 15) // 16
+    if h_out is None:
+        h_out = torch.zeros((lt, dim // 16, 16, 16), dtype=torch.float32, device=emb_tiles.device)
+    p = tc.TcEmbedParams()
+    p.l = lanes(rows)
+    p.embed, p.tokens, p.h, p.dim = ptr(emb_tiles), ptr(tokens), ptr(h_out), dim
+    tc.tc_embed(p)
+    return h_out
+
+
+def norm(h_tiles, rows: int, weight, eps: float, per_lane: bool = True, x_out=None):
+    """tc_norm: bf16 x tiles = RMSNorm(h tiles) * weight."""
+    if x_out is None:
+        x_out = torch.full(tuple(h_tiles.shape), 0x7FFF, dtype=U16, device=h_tiles.device)
+    p = tc.TcNormParams()
+    p.l = lanes(rows)
+    p.h, p.x, p.weight = ptr(h_tiles), ptr(x_out), ptr(weight)
+    p.dim, p.eps = int(h_tiles.shape[1]) * 16, eps
+    tc.tc_norm(p, per_lane)
+    return x_out
+
+
+def compact(in_tiles, lm_rows, out_tiles=None):
+    """tc_compact: out lane l <- in lane lm_rows[l]."""
+    count = int(lm_rows.numel())
+    if out_tiles is None:
+        out_tiles = torch.zeros(((count + 15) // 16, in_tiles.shape[1], 16, 16), dtype=U16, device=in_tiles.device)
+    p = tc.TcCompactParams()
+    p.l = lanes(int(in_tiles.shape[0]) * 16)
+    p.in_, p.out, p.lm_rows = ptr(in_tiles), ptr(out_tiles), ptr(lm_rows)
+    p.lm_count, p.col_tiles = count, int(in_tiles.shape[1])
+    tc.tc_compact(p)
+    return out_tiles
+
+
+def attention(q, kv: PagedKv, row_slot, row_pos, n_kv: int, head_dim: int, scale: float, layer: int = 0,
+              max_pages: int = 32, out_tiles=None, items=None, scratch=None):
+    """tc_attention over every page of every row (as the engine's item list,
+    src/engine.cpp:93-103). q: [rows][n_kv*4*head_dim] fp32. Returns bf16 x tiles."""
+    rows = int(q.shape[0])
+    cols = n_kv * 4 * head_dim
+    dev = q.device
+    if items is None:
+        pos = row_pos.cpu().tolist()
+        items = torch.tensor([[j, pg] for j in range(rows) for pg in range((pos[j] >> 6) + 1)], dtype=torch.int32,
+                             device=dev).reshape(-1)
+    rec = 4 * head_dim + 8
+    if scratch is None:
+        scratch = torch.zeros(rows * n_kv * max_pages * rec, dtype=torch.float32, device=dev)
+    if out_tiles is None:
+        out_tiles = torch.zeros(((rows + 15) // 16, cols // 16, 16, 16), dtype=U16, device=dev)
+    p = tc.AttentionParams()
+    p.l = lanes(rows)
+    p.q, p.q_stride, p.out, p.out_cols = ptr(q), cols, ptr(out_tiles), cols
+    p.kv = kv.ref
+    p.row_slot, p.row_pos, p.items, p.item_count = ptr(row_slot), ptr(row_pos), ptr(items), int(items.numel()) // 2
+    p.scratch, p.max_pages, p.rec_floats = ptr(scratch), max_pages, rec
+    p.layer, p.n_kv, p.n_q, p.head_dim, p.scale = layer, n_kv, 4, head_dim, scale
+    tc.tc_attention(p)
+    return out_tiles
+
+
 def qkv(wq_tiles, wk_tiles, wv_tiles, x_tiles, rows: int, head_dim: int, rope, row_slot, row_pos, kv: PagedKv,
         layer: int = 0, q_out=None):
     nq = wq_tiles.shape[0] * 16

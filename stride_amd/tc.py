@@ -7,6 +7,10 @@ Same names, same parameter blocks, same argument meaning as the reference:
     tc_mlp13(p, row_tiles, lane_tiles)         src/kernels_tc.h:84
     tc_lm_greedy(p, row_tiles, lane_tiles)     src/kernels_tc.h:86
     tc_lm_full(p, lane_tiles_per_block)        src/kernels_tc.h:87
+    tc_embed(p)                                src/kernels_tc.h:79
+    tc_norm(p, per_lane)                       src/kernels_tc.h:80
+    tc_attention(p)                            src/kernels_tc.h:82
+    tc_compact(p)                              src/kernels_tc.h:85
 
 Launches are asynchronous on ``kernel_stream()`` (the reference keeps one stream,
 src/kernels.cu:457-460); by default that is torch's current HIP stream. An error
@@ -19,13 +23,14 @@ from __future__ import annotations
 import ctypes as C
 
 from . import _lib
-from ._lib import (BestEntry, GemmMat, KvRef, Lanes, StrideTcError, TcGemmResidualParams, TcLmFullParams,
-                   TcLmGreedyParams, TcMlp13Params, TcQkvParams)
+from ._lib import (AttentionParams, BestEntry, GemmMat, KvRef, Lanes, StrideTcError, TcCompactParams, TcEmbedParams,
+                   TcGemmResidualParams, TcLmFullParams, TcLmGreedyParams, TcMlp13Params, TcNormParams, TcQkvParams)
 
 __all__ = [
     "BestEntry", "GemmMat", "KvRef", "Lanes", "StrideTcError", "TcGemmResidualParams", "TcLmFullParams",
     "TcLmGreedyParams", "TcMlp13Params", "TcQkvParams", "tc_qkv", "tc_gemm_residual", "tc_mlp13", "tc_lm_greedy",
-    "tc_lm_full", "kernel_stream", "set_kernel_stream", "mat", "lanes", "ptr", "split_count",
+    "tc_lm_full", "kernel_stream", "set_kernel_stream", "mat", "lanes", "ptr", "split_count", "AttentionParams",
+    "TcCompactParams", "TcEmbedParams", "TcNormParams", "tc_embed", "tc_norm", "tc_attention", "tc_compact",
 ]
 
 _stream = None  # None -> torch's current stream at call time
@@ -89,3 +94,19 @@ def tc_lm_greedy(p: TcLmGreedyParams, row_tiles_per_warp: int = 1, lane_tiles_pe
 
 def tc_lm_full(p: TcLmFullParams, lane_tiles_per_block: int = 1) -> None:
     _lib.check(_lib_().stride_tc_lm_full(C.byref(p), lane_tiles_per_block, kernel_stream()))
+
+
+def tc_embed(p: TcEmbedParams) -> None:
+    _lib.check(_lib_().stride_tc_embed(C.byref(p), kernel_stream()))
+
+
+def tc_norm(p: TcNormParams, per_lane: bool = True) -> None:
+    _lib.check(_lib_().stride_tc_norm(C.byref(p), 1 if per_lane else 0, kernel_stream()))
+
+
+def tc_attention(p: AttentionParams) -> None:
+    _lib.check(_lib_().stride_tc_attention(C.byref(p), kernel_stream()))
+
+
+def tc_compact(p: TcCompactParams) -> None:
+    _lib.check(_lib_().stride_tc_compact(C.byref(p), kernel_stream()))

@@ -36,6 +36,8 @@ PROBE = r"""
 int main() {
   printf("%zu %zu %zu %zu %zu %zu %zu %zu %zu %zu\n", sizeof(GM), sizeof(KV), sizeof(LN), sizeof(BE),
          sizeof(QKV), offsetof(QKV, kv), offsetof(QKV, head_dim), sizeof(RES), sizeof(MLP), sizeof(LMG));
+  printf("%zu %zu %zu %zu %zu %zu %zu %zu %zu\n", sizeof(EMB), sizeof(NRM), offsetof(NRM, eps), sizeof(CMP),
+         offsetof(CMP, col_tiles), sizeof(ATT), offsetof(ATT, kv), offsetof(ATT, items), offsetof(ATT, scale));
 }
 """
 
@@ -52,14 +54,18 @@ def _probe(tmp_path, include, names, extra=()):
 def test_struct_layout_matches_reference(tmp_path):
     ours = _probe(tmp_path, HEADER, dict(GM="StrideGemmMat", KV="StrideKvRef", LN="StrideLanes", BE="StrideBestEntry",
                                          QKV="StrideTcQkvParams", RES="StrideTcGemmResidualParams",
-                                         MLP="StrideTcMlp13Params", LMG="StrideTcLmGreedyParams"))
-    assert ours == ["16", "56", "16", "8", "176", "88", "172", "48", "64", "56"]
+                                         MLP="StrideTcMlp13Params", LMG="StrideTcLmGreedyParams",
+                                         EMB="StrideTcEmbedParams", NRM="StrideTcNormParams",
+                                         CMP="StrideTcCompactParams", ATT="StrideAttentionParams"))
+    assert ours == ["16", "56", "16", "8", "176", "88", "172", "48", "64", "56",
+                    "48", "48", "44", "48", "44", "176", "48", "120", "168"]
     if not os.path.exists(os.path.join(REF_SRC, "kernels_tc.h")):
         pytest.skip("reference tree absent")
     theirs = _probe(tmp_path, os.path.join(REF_SRC, "kernels_tc.h"),
                     dict(GM="stride::GemmMat", KV="stride::KvRef", LN="stride::Lanes", BE="stride::BestEntry",
                          QKV="stride::TcQkvParams", RES="stride::TcGemmResidualParams", MLP="stride::TcMlp13Params",
-                         LMG="stride::TcLmGreedyParams"))
+                         LMG="stride::TcLmGreedyParams", EMB="stride::TcEmbedParams", NRM="stride::TcNormParams",
+                         CMP="stride::TcCompactParams", ATT="stride::AttentionParams"))
     assert ours == theirs
 
 

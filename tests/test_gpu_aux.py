@@ -1,0 +1,113 @@
+"""GPU parity of the non-GEMM tensor-core operators (tc_embed, tc_norm,
+tc_attention, tc_compact) against the oracle, bit for bit, through the C ABI.
+Shapes follow the Llama-3.2-1B decode step (hidden 2048, 8 KV heads of 64 dims,
+four query heads per KV head); batches are ragged (not multiples of 16) and
+positions straddle the 64-position attention pages and the 16-token KV pages."""
+import numpy as np
+import pytest
+import torch
+
+from stride_amd import harness, layout
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+def bf16_bits(a):
+    return (np.ascontiguousarray(a, np.float32).view(np.uint32) >> 16).astype(np.uint16)
+
+
+def test_embed():
+    say("tc_embed M=37")
+    rng = np.random.default_rng(1)
+    vocab, dim, m = 4096, 2048, 37
+    emb = bf16_bits(rng.standard_normal((vocab, dim)) * 0.02)
+    tokens = rng.integers(0, vocab, m).astype(np.int32)
+    tiles = layout.pack_tiles(torch.from_numpy(emb.view(np.int16)).to(DEV))
+    h = harness.embed(tiles, torch.from_numpy(tokens).to(DEV), m, dim)
+    got = layout.untile_lanes(h, m).cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), emb[tokens].astype(np.uint32) << 16)
+
+
+@pytest.mark.parametrize("per_lane", [True, False])
+def test_norm(exact, per_lane):
+    say("tc_norm M=37 per_lane", per_lane)
+    rng = np.random.default_rng(2)
+    m, dim = 37, 2048
+    h = (rng.standard_normal((m, dim)) * 2).astype(np.float32)
+    w = rng.standard_normal(dim).astype(np.float32)
+    ht = layout.lane_tiles(torch.from_numpy(h).to(DEV))
+    x = harness.norm(ht, m, torch.from_numpy(w).to(DEV), 1e-5, per_lane=per_lane)
+    torch.cuda.synchronize()
+    xs = x.cpu()
+    got = layout.untile_lanes(xs, m).numpy().view(np.uint16)
+    assert np.array_equal(got, exact.tc_norm(h, w, 1e-5))
+    pad = layout.untile_lanes(xs, 48).numpy().view(np.uint16)[m:]
+    assert np.all(pad == (0x7FFF if per_lane else 0)), "padding lanes: untouched per lane, zeroed per tile"
+
+
+def test_norm_rows_are_batch_invariant(exact):
+    say("tc_norm invariance")
+    rng = np.random.default_rng(3)
+    h = rng.standard_normal((64, 2048)).astype(np.float32)
+    w = rng.standard_normal(2048).astype(np.float32)
+    wt = torch.from_numpy(w).to(DEV)
+    full = layout.untile_lanes(harness.norm(layout.lane_tiles(torch.from_numpy(h).to(DEV)), 64, wt, 1e-5), 64).cpu()
+    perm = rng.permutation(64)[:5]
+    part = layout.untile_lanes(harness.norm(layout.lane_tiles(torch.from_numpy(h[perm]).to(DEV)), 5, wt, 1e-5), 5).cpu()
+    assert torch.equal(part, full[perm])
+
+
+def test_compact():
+    say("tc_compact")
+    rng = np.random.default_rng(4)
+    m, dim = 70, 2048
+    x = bf16_bits(rng.standard_normal((m, dim)))
+    rows = np.array([3, 69, 0, 17, 17, 42], np.int32)
+    xt = layout.lane_tiles(torch.from_numpy(x.view(np.int16)).to(DEV))
+    out = harness.compact(xt, torch.from_numpy(rows).to(DEV))
+    got = layout.untile_lanes(out, rows.size).cpu().numpy().view(np.uint16)
+    assert np.array_equal(got, x[rows])
+
+
+@pytest.mark.parametrize("page_tokens", [16, 64])
+def test_attention(exact, page_tokens):
+    say("tc_attention page_tokens", page_tokens)
+    rng = np.random.default_rng(5 + page_tokens)
+    n_kv, hd, slots, cap, m = 8, 64, 6, 320, 21
+    q = rng.standard_normal((m, n_kv * 4, hd)).astype(np.float32)
+    k = bf16_bits(rng.standard_normal((slots, n_kv, cap, hd)))
+    v = bf16_bits(rng.standard_normal((slots, n_kv, cap, hd)))
+    slot = rng.permutation(slots)[rng.integers(0, slots, m)].astype(np.int32)
+    pos = rng.integers(0, cap, m).astype(np.int32)
+    pos[:7] = [0, 15, 16, 63, 64, 65, cap - 1]
+    kv = harness.PagedKv.create(slots, cap, n_kv, hd, 2, page_tokens, DEV, shuffle_seed=9)
+    kv.fill_dense(1, 0, torch.from_numpy(k.view(np.int16)))
+    kv.fill_dense(1, 1, torch.from_numpy(v.view(np.int16)))
+    scale = hd ** -0.5
+    out = harness.attention(torch.from_numpy(q.reshape(m, -1)).to(DEV), kv, torch.from_numpy(slot).to(DEV),
+                            torch.from_numpy(pos).to(DEV), n_kv, hd, scale, layer=1, max_pages=(cap + 63) // 64)
+    got = layout.untile_lanes(out, m).cpu().numpy().view(np.uint16)
+    want = exact.tc_attention(q, k, v, slot, pos, scale)
+    assert np.array_equal(got, want), f"{(got != want).sum()} mismatches"
+
+
+def test_attention_rejects_bad_arguments():
+    say("tc_attention rejects")
+    kv = harness.PagedKv.create(1, 64, 1, 64, 1, 16, DEV)
+    q = torch.zeros((1, 4 * 64), device=DEV)
+    z = torch.zeros(1, dtype=torch.int32, device=DEV)
+    from stride_amd import _lib, tc
+    p = tc.AttentionParams()
+    p.l = tc.lanes(1)
+    p.q, p.q_stride, p.out, p.out_cols = tc.ptr(q), 256, tc.ptr(q), 256
+    p.kv = kv.ref
+    p.row_slot = p.row_pos = p.items = tc.ptr(z)
+    p.item_count, p.scratch, p.max_pages, p.rec_floats = 1, tc.ptr(q), 1, 264
+    p.n_kv, p.n_q, p.head_dim, p.scale = 1, 2, 64, 0.125
+    with pytest.raises(_lib.StrideTcError, match="four query heads"):
+        tc.tc_attention(p)
