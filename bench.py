@@ -43,6 +43,8 @@ def parse():
     ap.add_argument("--table", type=int, default=1, help="per-GEMM table over M (0 to skip)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline budget (0 to skip)")
     ap.add_argument("--cpu-threads", type=int, default=16)
+    ap.add_argument("--engine", type=int, default=1,
+                    help="also time one full decode step of the config-5 engine (0 to skip)")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="also run one plain device copy of this size (calibrates FETCH_SIZE/WRITE_SIZE counters)")
     return ap.parse_args()
@@ -248,6 +250,37 @@ def cpu_baseline(seconds, threads):
             "per_gemm_ms": {k: round(v * 1e3, 3) for k, v in t.items()}}
 
 
+def engine_step(torch, dev, m, steps, warmup, position=383):
+    """BASELINE config 5's decode step at batch m: the whole step of
+    stride_amd.engine (embedding, per layer RMSNorm, QKV + RoPE + KV append,
+    paged attention over `position` + 1 positions, O, RMSNorm, gate/up, down;
+    final RMSNorm and the greedy LM head), every row at `position` (the middle of
+    a 256-token prompt + 256-token generation), captured as one HIP graph and
+    replayed. Random-init weights; KV contents do not change the work."""
+    from stride_amd import engine
+
+    w = engine.Weights(engine.LlamaConfig(), dev, seed=1, max_positions=512)
+    eng = engine.Engine(w, slots=m, max_ctx=512, max_rows=m, page_tokens=16, shuffle_seed=3)
+    rows = [(j, position, (j * 7919) % w.cfg.vocab) for j in range(m)]
+    slot, pos, tok, items = eng.device_rows(rows)
+    best = torch.empty((m, 2), dtype=torch.int32, device=dev)
+    g = capture(torch, [lambda: eng.launch(m, slot, pos, tok, items, best=best)])
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        g.replay()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    del g, eng, w
+    torch.cuda.empty_cache()
+    return {"batch": m, "position": position, "page_tokens": 16, "ms_per_step": round(dt / steps * 1e3, 4),
+            "tok_s": round(m * steps / dt, 1), "launch": "HIP graph of one full step, replayed",
+            "ops": "tc_embed, 16 x (tc_norm, tc_qkv, tc_attention, tc_gemm_residual, tc_norm, tc_mlp13, "
+                   "tc_gemm_residual), tc_norm, tc_lm_greedy"}
+
+
 def main():
     a = parse()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -331,6 +364,7 @@ def main():
             del bm
             torch.cuda.empty_cache()
 
+    full = engine_step(torch, dev, a.m, a.steps, a.warmup) if a.engine else None
     cpu = cpu_baseline(a.cpu_seconds, a.cpu_threads) if a.cpu_seconds > 0 else None
     out = {
         "metric": "Llama-3.2-1B GEMM GB/s & TFLOP/s (% roofline) at M=1..4096; decode tok/s",
@@ -341,7 +375,7 @@ def main():
                    "M": a.m, "layers": LAYERS, "weight_bytes_per_step": int(weight_bytes),
                    "step_GB/s": round(weight_bytes / (ms_step / 1e3) / 1e9, 1), "parallelism": "single-gpu",
                    "launch": "HIP graph of one step, replayed", "eager_ms_per_step": round(eager_ms, 4)},
-        "roofline": roof, "cpu_baseline": cpu, "gemm_table": table,
+        "roofline": roof, "cpu_baseline": cpu, "full_decode_step": full, "gemm_table": table,
     }
     print(json.dumps(out), flush=True)
 

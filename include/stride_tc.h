@@ -217,7 +217,8 @@ int stride_tc_norm(const StrideTcNormParams* p, int per_lane, void* stream);
  * on its own into a record (max, denominator, weighted values) in `scratch`;
  * then each row's pages are combined in ascending order and the output is
  * written as bf16 x tiles. The KV storage page (group_elems / head_dim tokens,
- * a power of two) is independent of the 64-position summation page. */
+ * a power of two) is independent of the 64-position summation page. head_dim
+ * must be 32, 64 or 128; n_q must be 4. */
 int stride_tc_attention(const StrideAttentionParams* p, void* stream);
 
 /* Replaces stride::tc_compact (src/kernels_tc.h:85, src/kernels_tc.cu:566-587):

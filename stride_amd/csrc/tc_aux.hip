@@ -26,7 +26,6 @@ namespace {
 // constant of the tree, independent of the KV storage page size.
 constexpr int kAttnPageShift = 6;
 constexpr int kAttnPage = 1 << kAttnPageShift;
-constexpr int kMaxHeadDim = 128;
 constexpr int kHeadsPerGroup = 4;  // the reference's float4 query packing
 
 // ---------------------------------------------------------------------------
@@ -145,14 +144,19 @@ __device__ __forceinline__ const uint16_t* kv_row(const StrideKvRef& kv, int pag
          which * kv.which_elems + group * kv.group_elems + static_cast<int64_t>(token) * kv.head_dim;
 }
 
-__device__ __forceinline__ float bf16_at(const uint16_t* row, int d) { return f32_of(static_cast<uint32_t>(row[d]) << 16); }
-
-// One (row, page) item for one KV group (src/kernel_common.h:84-250). Lane i
-// scores position p0 + i for the four query heads (an fmaf chain over the head
-// dims in order, then times scale); the page maximum is order-free; the
-// exponentials follow; lanes 0..3 add one head's weights left to right; each
-// lane then mixes the values of its dims over the positions in order.
+// One (row, page) item for one KV group (src/kernel_common.h:84-250). The page's
+// V rows are fetched with 16-byte loads and parked in LDS, and each lane's K row
+// is fetched whole, so both latencies overlap. Lane i scores position p0 + i for
+// the four query heads (an fmaf chain over the head dims in order, then times
+// scale); the page maximum is order-free; the exponentials follow. Each lane
+// then mixes the values of its dims over the positions in order; in the same
+// pass it adds the weights left to right, which yields the denominators (the
+// add and the mix see the weights in the same order) without a serial phase.
+template <int D>
 __global__ __launch_bounds__(64) void k_attn_page(StrideAttentionParams p, int page_shift) {
+  constexpr int kPieces = kAttnPage * D / 8;  // 16-byte pieces of one page of V
+  constexpr int kPer = kPieces / 64;          // per lane
+  constexpr int kKey = D / 8;                 // 16-byte pieces of one K row
   const int item = blockIdx.x / p.n_kv;
   const int g = blockIdx.x % p.n_kv;
   const int lane = threadIdx.x;
@@ -162,68 +166,88 @@ __global__ __launch_bounds__(64) void k_attn_page(StrideAttentionParams p, int p
   const int visible = p.row_pos[j] + 1;
   const int p0 = page << kAttnPageShift;
   const int n = min(visible - p0, kAttnPage);
-  const int D = p.head_dim;
-  __shared__ float q[kHeadsPerGroup][kMaxHeadDim];
-  __shared__ float w[kHeadsPerGroup][kAttnPage];
-  __shared__ float mm[kHeadsPerGroup], den[kHeadsPerGroup];
+  __shared__ f32x4 q4[D];        // the four heads' query values, per dim
+  __shared__ f32x4 w4[kAttnPage];  // the four heads' weights, per position
+  __shared__ uint16_t vs[kAttnPage][D];
 
+  // Positions past the row's last one are clamped to it (their values are never
+  // used), so every load is unconditional and stays inside the row's own pages.
+  const int last = visible - 1;
+  u32x4 vr[kPer], kr[kKey];
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int P = k * 64 + lane, i = P / (D / 8), c = P % (D / 8);
+    vr[k] = load16(kv_row(p.kv, page_shift, p.layer, 1, g, slot, min(p0 + i, last)) + c * 8);
+  }
+  {
+    const uint16_t* key = kv_row(p.kv, page_shift, p.layer, 0, g, slot, min(p0 + lane, last));
+#pragma unroll
+    for (int c = 0; c < kKey; ++c) kr[c] = load16(key + 8 * c);
+  }
   const float* qrow = p.q + static_cast<int64_t>(j) * p.q_stride + static_cast<int64_t>(g * kHeadsPerGroup) * D;
-  for (int i = lane; i < kHeadsPerGroup * D; i += 64) q[i / D][i % D] = qrow[i];
+  for (int d = lane; d < D; d += 64)
+    q4[d] = f32x4{qrow[d], qrow[D + d], qrow[2 * D + d], qrow[3 * D + d]};
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int P = k * 64 + lane;
+    *reinterpret_cast<u32x4*>(&vs[P / (D / 8)][(P % (D / 8)) * 8]) = vr[k];
+  }
   __syncthreads();
 
-  const float neg_inf = f32_of(0xFF800000u);
-  float sc[kHeadsPerGroup];
+  float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
 #pragma unroll
-  for (int h = 0; h < kHeadsPerGroup; ++h) sc[h] = neg_inf;
-  if (lane < n) {
-    const uint16_t* key = kv_row(p.kv, page_shift, p.layer, 0, g, slot, p0 + lane);
-    float a[kHeadsPerGroup] = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int d = 0; d < D; d += 8) {
-      const u32x4 kw = load16(key + d);
+  for (int c = 0; c < kKey; ++c) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float k = f32_of(e & 1 ? kw[e >> 1] & 0xFFFF0000u : kw[e >> 1] << 16);
-#pragma unroll
-        for (int h = 0; h < kHeadsPerGroup; ++h) a[h] = __builtin_fmaf(q[h][d + e], k, a[h]);
-      }
+    for (int e = 0; e < 8; ++e) {
+      const float k = f32_of(e & 1 ? kr[c][e >> 1] & 0xFFFF0000u : kr[c][e >> 1] << 16);
+      const f32x4 qd = q4[8 * c + e];
+      a0 = __builtin_fmaf(qd[0], k, a0);
+      a1 = __builtin_fmaf(qd[1], k, a1);
+      a2 = __builtin_fmaf(qd[2], k, a2);
+      a3 = __builtin_fmaf(qd[3], k, a3);
     }
-#pragma unroll
-    for (int h = 0; h < kHeadsPerGroup; ++h) sc[h] = a[h] * p.scale;
+    __builtin_amdgcn_sched_barrier(0);  // keep each chunk's query reads next to their use
   }
-  // Page maximum (a max is independent of the order it is taken in).
+  const float neg_inf = f32_of(0xFF800000u);
+  float sc[kHeadsPerGroup] = {a0 * p.scale, a1 * p.scale, a2 * p.scale, a3 * p.scale};
+  f32x4 mx;
 #pragma unroll
   for (int h = 0; h < kHeadsPerGroup; ++h) {
+    if (lane >= n) sc[h] = neg_inf;
     float m = sc[h];
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
       const float o = __shfl_xor(m, off);
       if (o > m) m = o;
     }
-    if (lane < n) w[h][lane] = det_exp(sc[h] - m);
-    if (lane == 0) mm[h] = m;
+    mx[h] = m;
   }
-  __syncthreads();
-  if (lane < kHeadsPerGroup) {
-    float s = 0.0f;
-    for (int i = 0; i < n; ++i) s = s + w[lane][i];
-    den[lane] = s;
-  }
+  if (lane < n) w4[lane] = f32x4{det_exp(sc[0] - mx[0]), det_exp(sc[1] - mx[1]), det_exp(sc[2] - mx[2]), det_exp(sc[3] - mx[3])};
   __syncthreads();
   float* rec = p.scratch + (static_cast<int64_t>(j * p.n_kv + g) * p.max_pages + page) * p.rec_floats;
-  if (lane < kHeadsPerGroup) {
-    rec[lane] = mm[lane];
-    rec[4 + lane] = den[lane];
-  }
   float* v_out = rec + 8;
-  for (int d = lane; d < D; d += 64) {
-    float a[kHeadsPerGroup] = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int i = 0; i < n; ++i) {
-      const float v = bf16_at(kv_row(p.kv, page_shift, p.layer, 1, g, slot, p0 + i), d);
 #pragma unroll
-      for (int h = 0; h < kHeadsPerGroup; ++h) a[h] = __builtin_fmaf(w[h][i], v, a[h]);
+  for (int d = lane; d < D; d += 64) {
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f}, den = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 4
+    for (int i = 0; i < n; ++i) {
+      const float v = f32_of(static_cast<uint32_t>(vs[i][d]) << 16);
+      const f32x4 wi = w4[i];
+#pragma unroll
+      for (int h = 0; h < kHeadsPerGroup; ++h) {
+        acc[h] = __builtin_fmaf(wi[h], v, acc[h]);
+        den[h] = den[h] + wi[h];
+      }
     }
 #pragma unroll
-    for (int h = 0; h < kHeadsPerGroup; ++h) v_out[h * D + d] = a[h];
+    for (int h = 0; h < kHeadsPerGroup; ++h) v_out[h * D + d] = acc[h];
+    if (d == 0) {
+#pragma unroll
+      for (int h = 0; h < kHeadsPerGroup; ++h) {
+        rec[h] = mx[h];
+        rec[4 + h] = den[h];
+      }
+    }
   }
 }
 
@@ -322,7 +346,7 @@ int stride_tc_attention(const StrideAttentionParams* p, void* stream) {
   while (page_shift < 30 && (int64_t{1} << page_shift) < page_tokens) ++page_shift;
   std::string why;
   if (!lanes_valid(p->l)) why = "lane_groups must equal ceil(rows/16)";
-  else if (D <= 0 || D > kMaxHeadDim || D % 16 != 0 || p->kv.head_dim != D) why = "head_dim must be a multiple of 16 up to 128 and match kv.head_dim";
+  else if ((D != 32 && D != 64 && D != 128) || p->kv.head_dim != D) why = "head_dim must be 32, 64 or 128 and match kv.head_dim";
   else if (p->n_q != kHeadsPerGroup) why = "four query heads per KV group are required (the reference packs them in a float4)";
   else if (p->n_kv <= 0 || p->rec_floats < 8 + 4 * D || p->max_pages <= 0 || p->item_count < 0) why = "bad n_kv, rec_floats, max_pages or item_count";
   else if (page_tokens <= 0 || (int64_t{1} << page_shift) != page_tokens) why = "the KV storage page (group_elems / head_dim) must be a power of two";
@@ -335,7 +359,11 @@ int stride_tc_attention(const StrideAttentionParams* p, void* stream) {
   if (p->l.rows == 0) return 0;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (p->item_count > 0) {
-    hipLaunchKernelGGL(k_attn_page, dim3(p->item_count * p->n_kv), dim3(64), 0, st, *p, page_shift);
+    const dim3 grid(p->item_count * p->n_kv);
+    if (D == 32) hipLaunchKernelGGL(k_attn_page<32>, grid, dim3(64), 0, st, *p, page_shift);
+    else if (D == 64) hipLaunchKernelGGL(k_attn_page<64>, grid, dim3(64), 0, st, *p, page_shift);
+    else if (D == 128) hipLaunchKernelGGL(k_attn_page<128>, grid, dim3(64), 0, st, *p, page_shift);
+    else return fail(STRIDE_TC_EINVAL, "tc_attention: head_dim must be 32, 64 or 128");
     if (int rc = launched("tc_attention (pages)")) return rc;
   }
   hipLaunchKernelGGL(k_attn_combine, dim3(p->l.rows * p->n_kv), dim3(64), p->max_pages * 4 * sizeof(float), st, *p);
