@@ -58,18 +58,35 @@ __global__ __launch_bounds__(256) void k_embed(StrideTcEmbedParams p) {
 // ---------------------------------------------------------------------------
 // RMSNorm, one wave per lane. Lanes 0..31 of the wave compute the reference's
 // 32 partials (partial t: fmaf over columns 0..15 of column tiles ct == t mod
-// 32, ascending); lane 0 adds them left to right; every lane then writes its
-// column tiles as bf16(g * (v * r)) (src/kernels_tc.cu:205-271, 276-340).
+// 32, ascending); lane 0 adds them left to right; then x = bf16(g * (v * r))
+// (src/kernels_tc.cu:205-271, 276-340). With TPL > 0 (dim == 32 * 16 * TPL)
+// each of lanes 0..31 keeps its TPL tiles and their gains in registers, so h
+// is read once; TPL == 0 is the general form.
+template <int TPL>
 __global__ __launch_bounds__(64) void k_norm(StrideTcNormParams p, int per_lane) {
   const int b = blockIdx.x;  // lane index in [0, lane_groups * 16)
   const int lane = threadIdx.x;
   const int lt = b >> 4, j = b & 15;
   const int col_tiles = p.dim >> 4;
   const int64_t row0 = static_cast<int64_t>(lt) * col_tiles * kTileElems + j * 16;
+  auto tile = [&](int ct) { return row0 + static_cast<int64_t>(ct) * kTileElems; };
+  auto store = [&](int ct, const f32x4* v, const f32x4* g, float r) {
+    uint32_t o[8];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t b0 = bf16_rne(g[q][0] * (v[q][0] * r)), b1 = bf16_rne(g[q][1] * (v[q][1] * r));
+      const uint32_t b2 = bf16_rne(g[q][2] * (v[q][2] * r)), b3 = bf16_rne(g[q][3] * (v[q][3] * r));
+      o[2 * q] = b0 | (b1 << 16);
+      o[2 * q + 1] = b2 | (b3 << 16);
+    }
+    u32x4* out = reinterpret_cast<u32x4*>(p.x + tile(ct));
+    out[0] = u32x4{o[0], o[1], o[2], o[3]};
+    out[1] = u32x4{o[4], o[5], o[6], o[7]};
+  };
   if (b >= p.l.rows) {
     if (per_lane) return;
     for (int ct = lane; ct < col_tiles; ct += 64) {
-      u32x4* out = reinterpret_cast<u32x4*>(p.x + row0 + static_cast<int64_t>(ct) * kTileElems);
+      u32x4* out = reinterpret_cast<u32x4*>(p.x + tile(ct));
       out[0] = u32x4{0u, 0u, 0u, 0u};
       out[1] = u32x4{0u, 0u, 0u, 0u};
     }
@@ -77,42 +94,68 @@ __global__ __launch_bounds__(64) void k_norm(StrideTcNormParams p, int per_lane)
   }
   __shared__ float partial[32];
   __shared__ float rs;
-  if (lane < 32) {
-    float acc = 0.0f;
-    for (int ct = lane; ct < col_tiles; ct += 32) {
-      const f32x4* v = reinterpret_cast<const f32x4*>(p.h + row0 + static_cast<int64_t>(ct) * kTileElems);
+  if constexpr (TPL > 0) {
+    f32x4 v[TPL][4], g[TPL][4];
+    if (lane < 32) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const f32x4 w = v[q];
+      for (int k = 0; k < TPL; ++k) {
+        const f32x4* src = reinterpret_cast<const f32x4*>(p.h + tile(lane + 32 * k));
+        const f32x4* gs = reinterpret_cast<const f32x4*>(p.weight + (lane + 32 * k) * 16);
 #pragma unroll
-        for (int c = 0; c < 4; ++c) acc = __builtin_fmaf(w[c], w[c], acc);
+        for (int q = 0; q < 4; ++q) {
+          v[k][q] = src[q];
+          g[k][q] = gs[q];
+        }
       }
-    }
-    partial[lane] = acc;
-  }
-  __syncthreads();
-  if (lane == 0) {
-    float sum = partial[0];
-    for (int i = 1; i < 32; ++i) sum = sum + partial[i];
-    rs = 1.0f / sqrtf(sum / static_cast<float>(p.dim) + p.eps);
-  }
-  __syncthreads();
-  const float r = rs;
-  for (int ct = lane; ct < col_tiles; ct += 64) {
-    const f32x4* v = reinterpret_cast<const f32x4*>(p.h + row0 + static_cast<int64_t>(ct) * kTileElems);
-    const f32x4* gv = reinterpret_cast<const f32x4*>(p.weight + ct * 16);
-    uint32_t o[8];
+      float acc = 0.0f;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const f32x4 w = v[q], g = gv[q];
-      const uint32_t b0 = bf16_rne(g[0] * (w[0] * r)), b1 = bf16_rne(g[1] * (w[1] * r));
-      const uint32_t b2 = bf16_rne(g[2] * (w[2] * r)), b3 = bf16_rne(g[3] * (w[3] * r));
-      o[2 * q] = b0 | (b1 << 16);
-      o[2 * q + 1] = b2 | (b3 << 16);
+      for (int k = 0; k < TPL; ++k)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int c = 0; c < 4; ++c) acc = __builtin_fmaf(v[k][q][c], v[k][q][c], acc);
+      partial[lane] = acc;
     }
-    u32x4* out = reinterpret_cast<u32x4*>(p.x + row0 + static_cast<int64_t>(ct) * kTileElems);
-    out[0] = u32x4{o[0], o[1], o[2], o[3]};
-    out[1] = u32x4{o[4], o[5], o[6], o[7]};
+    __syncthreads();
+    if (lane == 0) {
+      float sum = partial[0];
+      for (int i = 1; i < 32; ++i) sum = sum + partial[i];
+      rs = 1.0f / sqrtf(sum / static_cast<float>(p.dim) + p.eps);
+    }
+    __syncthreads();
+    if (lane < 32) {
+      const float r = rs;
+#pragma unroll
+      for (int k = 0; k < TPL; ++k) store(lane + 32 * k, v[k], g[k], r);
+    }
+  } else {
+    if (lane < 32) {
+      float acc = 0.0f;
+      for (int ct = lane; ct < col_tiles; ct += 32) {
+        const f32x4* v = reinterpret_cast<const f32x4*>(p.h + tile(ct));
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const f32x4 w = v[q];
+#pragma unroll
+          for (int c = 0; c < 4; ++c) acc = __builtin_fmaf(w[c], w[c], acc);
+        }
+      }
+      partial[lane] = acc;
+    }
+    __syncthreads();
+    if (lane == 0) {
+      float sum = partial[0];
+      for (int i = 1; i < 32; ++i) sum = sum + partial[i];
+      rs = 1.0f / sqrtf(sum / static_cast<float>(p.dim) + p.eps);
+    }
+    __syncthreads();
+    const float r = rs;
+    for (int ct = lane; ct < col_tiles; ct += 64) {
+      const f32x4* v = reinterpret_cast<const f32x4*>(p.h + tile(ct));
+      const f32x4* gv = reinterpret_cast<const f32x4*>(p.weight + ct * 16);
+      const f32x4 vv[4] = {v[0], v[1], v[2], v[3]}, gg[4] = {gv[0], gv[1], gv[2], gv[3]};
+      store(ct, vv, gg, r);
+    }
   }
 }
 
@@ -252,43 +295,47 @@ __global__ __launch_bounds__(64) void k_attn_page(StrideAttentionParams p, int p
 }
 
 // Ascending-page combine of one row's records for one KV group, written as bf16
-// x tiles (src/kernel_common.h:252-309, writer src/kernels_tc.cu:658-666).
-__global__ __launch_bounds__(64) void k_attn_combine(StrideAttentionParams p) {
-  extern __shared__ float f[];  // [4][max_pages]
+// x tiles (src/kernel_common.h:252-309, writer src/kernels_tc.cu:658-666). All
+// of the row's records come into LDS in one coalesced pass; threads 0..3 derive
+// each head's page factors and denominator (pages in order); thread (h, d) then
+// folds the weighted values of head h, dim d over the pages in order.
+template <int D>
+__global__ __launch_bounds__(256) void k_attn_combine(StrideAttentionParams p) {
+  extern __shared__ float recs[];  // [pages][rec_floats], then f[4][pages]
   __shared__ float den[kHeadsPerGroup];
   const int j = blockIdx.x / p.n_kv;
   const int g = blockIdx.x % p.n_kv;
-  const int lane = threadIdx.x;
+  const int t = threadIdx.x;
   const int pages = (p.row_pos[j] >> kAttnPageShift) + 1;
-  const int D = p.head_dim;
-  const float* recs = p.scratch + static_cast<int64_t>(j * p.n_kv + g) * p.max_pages * p.rec_floats;
-  if (lane < kHeadsPerGroup) {
+  const int rf = p.rec_floats;
+  const float* src = p.scratch + static_cast<int64_t>(j * p.n_kv + g) * p.max_pages * rf;
+  for (int i = t; i < pages * rf; i += 256) recs[i] = src[i];
+  float* f = recs + pages * rf;
+  __syncthreads();
+  if (t < kHeadsPerGroup) {
     float m = f32_of(0xFF800000u);
     for (int c = 0; c < pages; ++c) {
-      const float mc = recs[static_cast<int64_t>(c) * p.rec_floats + lane];
+      const float mc = recs[c * rf + t];
       if (mc > m) m = mc;
     }
     float d = 0.0f;
     for (int c = 0; c < pages; ++c) {
-      const float* rec = recs + static_cast<int64_t>(c) * p.rec_floats;
-      const float e = det_exp(rec[lane] - m);
-      f[lane * p.max_pages + c] = e;
-      d = __builtin_fmaf(e, rec[4 + lane], d);
+      const float e = det_exp(recs[c * rf + t] - m);
+      f[t * pages + c] = e;
+      d = __builtin_fmaf(e, recs[c * rf + 4 + t], d);
     }
-    den[lane] = d;
+    den[t] = d;
   }
   __syncthreads();
   const int col_tiles = p.out_cols >> 4;
   uint16_t* out = static_cast<uint16_t*>(p.out);
   const int64_t lane0 = static_cast<int64_t>(j >> 4) * col_tiles * kTileElems + (j & 15) * 16;
-  for (int d = lane; d < D; d += 64) {
-    for (int qh = 0; qh < p.n_q; ++qh) {
-      float acc = 0.0f;
-      for (int c = 0; c < pages; ++c)
-        acc = __builtin_fmaf(f[qh * p.max_pages + c], recs[static_cast<int64_t>(c) * p.rec_floats + 8 + qh * D + d], acc);
-      const int idx = (g * p.n_q + qh) * D + d;
-      out[lane0 + static_cast<int64_t>(idx >> 4) * kTileElems + (idx & 15)] = static_cast<uint16_t>(bf16_rne(acc / den[qh]));
-    }
+  for (int hd = t; hd < p.n_q * D; hd += 256) {
+    const int qh = hd / D, d = hd % D;
+    float acc = 0.0f;
+    for (int c = 0; c < pages; ++c) acc = __builtin_fmaf(f[qh * pages + c], recs[c * rf + 8 + qh * D + d], acc);
+    const int idx = (g * p.n_q + qh) * D + d;
+    out[lane0 + static_cast<int64_t>(idx >> 4) * kTileElems + (idx & 15)] = static_cast<uint16_t>(bf16_rne(acc / den[qh]));
   }
 }
 
@@ -304,6 +351,26 @@ static_assert(sizeof(StrideTcNormParams) == 48, "TcNormParams layout");
 static_assert(sizeof(StrideTcCompactParams) == 48, "TcCompactParams layout");
 static_assert(offsetof(StrideAttentionParams, kv) == 48 && sizeof(StrideAttentionParams) == 176,
               "AttentionParams layout");
+
+static int launched(const char* what);
+
+// The combine keeps a row's records in LDS; past the default 64 KiB of dynamic
+// LDS (long contexts at head_dim 128) the kernel's limit is raised once.
+// (The kernel's own static LDS shares the 160 KiB, hence the margin.)
+constexpr size_t kCombineLdsMax = 159 * 1024;
+
+template <int D>
+static int combine(dim3 grid, size_t lds, hipStream_t st, const StrideAttentionParams& p) {
+  static size_t raised = 64 * 1024;
+  if (lds > raised) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn_combine<D>),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    if (e != hipSuccess) return fail(static_cast<int>(e), std::string("tc_attention: raising the LDS limit failed: ") + hipGetErrorString(e));
+    raised = lds;
+  }
+  hipLaunchKernelGGL(k_attn_combine<D>, grid, dim3(256), lds, st, p);
+  return launched("tc_attention (combine)");
+}
 
 static int launched(const char* what) {
   const hipError_t e = hipGetLastError();
@@ -326,7 +393,16 @@ int stride_tc_norm(const StrideTcNormParams* p, int per_lane, void* stream) {
       (p->l.rows > 0 && (!p->h || !p->x || !p->weight)))
     return fail(STRIDE_TC_EINVAL, "tc_norm: need rows >= 0, lane_groups = ceil(rows/16), dim a positive multiple of 16 and pointers");
   if (p->l.rows == 0) return 0;
-  hipLaunchKernelGGL(k_norm, dim3(p->l.lane_groups * 16), dim3(64), 0, static_cast<hipStream_t>(stream), *p, per_lane ? 1 : 0);
+  const dim3 grid(p->l.lane_groups * 16);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int pl = per_lane ? 1 : 0;
+  switch (p->dim) {
+    case 512: hipLaunchKernelGGL(k_norm<1>, grid, dim3(64), 0, st, *p, pl); break;
+    case 1024: hipLaunchKernelGGL(k_norm<2>, grid, dim3(64), 0, st, *p, pl); break;
+    case 2048: hipLaunchKernelGGL(k_norm<4>, grid, dim3(64), 0, st, *p, pl); break;
+    case 4096: hipLaunchKernelGGL(k_norm<8>, grid, dim3(64), 0, st, *p, pl); break;
+    default: hipLaunchKernelGGL(k_norm<0>, grid, dim3(64), 0, st, *p, pl); break;
+  }
   return launched("tc_norm");
 }
 
@@ -354,7 +430,8 @@ int stride_tc_attention(const StrideAttentionParams* p, void* stream) {
   else if (p->l.rows > 0 && (!p->q || !p->out || !p->kv.arena || !p->kv.table || !p->row_slot || !p->row_pos || !p->scratch ||
                              (p->item_count > 0 && !p->items)))
     why = "missing pointer";
-  else if (static_cast<size_t>(p->max_pages) * 4 * sizeof(float) > 64 * 1024) why = "max_pages too large for the combine's LDS";
+  else if (static_cast<size_t>(p->max_pages) * (p->rec_floats + kHeadsPerGroup) * sizeof(float) > kCombineLdsMax)
+    why = "max_pages * rec_floats too large for the combine's LDS (159 KiB)";
   if (!why.empty()) return fail(STRIDE_TC_EINVAL, "tc_attention: " + why);
   if (p->l.rows == 0) return 0;
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -366,8 +443,11 @@ int stride_tc_attention(const StrideAttentionParams* p, void* stream) {
     else return fail(STRIDE_TC_EINVAL, "tc_attention: head_dim must be 32, 64 or 128");
     if (int rc = launched("tc_attention (pages)")) return rc;
   }
-  hipLaunchKernelGGL(k_attn_combine, dim3(p->l.rows * p->n_kv), dim3(64), p->max_pages * 4 * sizeof(float), st, *p);
-  return launched("tc_attention (combine)");
+  const size_t lds = static_cast<size_t>(p->max_pages) * (p->rec_floats + kHeadsPerGroup) * sizeof(float);
+  const dim3 cgrid(p->l.rows * p->n_kv);
+  if (D == 32) return combine<32>(cgrid, lds, st, *p);
+  if (D == 64) return combine<64>(cgrid, lds, st, *p);
+  return combine<128>(cgrid, lds, st, *p);
 }
 
 }  // extern "C"

@@ -33,11 +33,11 @@ def test_embed():
     assert np.array_equal(got.view(np.uint32), emb[tokens].astype(np.uint32) << 16)
 
 
-@pytest.mark.parametrize("per_lane", [True, False])
-def test_norm(exact, per_lane):
-    say("tc_norm M=37 per_lane", per_lane)
+@pytest.mark.parametrize("per_lane,dim", [(True, 2048), (False, 2048), (True, 768), (False, 512)])
+def test_norm(exact, per_lane, dim):
+    say("tc_norm M=37 per_lane", per_lane, "dim", dim)
     rng = np.random.default_rng(2)
-    m, dim = 37, 2048
+    m = 37
     h = (rng.standard_normal((m, dim)) * 2).astype(np.float32)
     w = rng.standard_normal(dim).astype(np.float32)
     ht = layout.lane_tiles(torch.from_numpy(h).to(DEV))
@@ -74,17 +74,18 @@ def test_compact():
     assert np.array_equal(got, x[rows])
 
 
-@pytest.mark.parametrize("page_tokens", [16, 64])
-def test_attention(exact, page_tokens):
-    say("tc_attention page_tokens", page_tokens)
-    rng = np.random.default_rng(5 + page_tokens)
-    n_kv, hd, slots, cap, m = 8, 64, 6, 320, 21
+@pytest.mark.parametrize("page_tokens,n_kv,hd,cap,m", [(16, 8, 64, 320, 21), (64, 8, 64, 320, 21),
+                                                        (16, 2, 128, 2048, 3), (32, 1, 32, 200, 9)])
+def test_attention(exact, page_tokens, n_kv, hd, cap, m):
+    say("tc_attention page_tokens", page_tokens, "n_kv", n_kv, "hd", hd, "cap", cap, "m", m)
+    rng = np.random.default_rng(5 + page_tokens + hd)
+    slots = 6
     q = rng.standard_normal((m, n_kv * 4, hd)).astype(np.float32)
     k = bf16_bits(rng.standard_normal((slots, n_kv, cap, hd)))
     v = bf16_bits(rng.standard_normal((slots, n_kv, cap, hd)))
     slot = rng.permutation(slots)[rng.integers(0, slots, m)].astype(np.int32)
     pos = rng.integers(0, cap, m).astype(np.int32)
-    pos[:7] = [0, 15, 16, 63, 64, 65, cap - 1]
+    pos[:min(m, 7)] = np.array([cap - 1, 0, 15, 16, 63, 64, 65])[:min(m, 7)]
     kv = harness.PagedKv.create(slots, cap, n_kv, hd, 2, page_tokens, DEV, shuffle_seed=9)
     kv.fill_dense(1, 0, torch.from_numpy(k.view(np.int16)))
     kv.fill_dense(1, 1, torch.from_numpy(v.view(np.int16)))
