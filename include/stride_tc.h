@@ -122,6 +122,15 @@ typedef struct StrideTcLmFullParams {
   float* logits;
 } StrideTcLmFullParams;
 
+/* No reference counterpart: parameters of stride_tc_gemm_f32x. */
+typedef struct StrideTcGemmF32xParams {
+  StrideLanes l;
+  const float* x;      /* fp32 activations, row-major [rows][cols] */
+  StrideGemmMat m;
+  float* y;            /* fp32 output tiles [lt][rt][16 lanes][16 rows] (the h layout), overwritten */
+  uint16_t* workspace; /* caller-owned, 2 * lane_groups * 16 * cols bf16 elements */
+} StrideTcGemmF32xParams;
+
 /* src/kernels_tc.h:10-16 */
 typedef struct StrideTcEmbedParams {
   StrideLanes l;
@@ -199,6 +208,14 @@ int stride_tc_lm_greedy(const StrideTcLmGreedyParams* p, int row_tiles_per_warp,
 /* Replaces stride::tc_lm_full (src/kernels_tc.h:87, src/kernels_tc.cu:707-710):
  * logits tiles [row tile][lane tile][16 rows][16 lanes], fp32. */
 int stride_tc_lm_full(const StrideTcLmFullParams* p, int lane_tiles_per_block, void* stream);
+
+/* No reference counterpart (the reference's tensor-core path consumes bf16 x
+ * only): y = W x for fp32 activations, for callers that keep them in fp32 (a
+ * projection compared against the CPU exact path, which reads fp32 x). x is split
+ * into hi = bf16(x) and lo = bf16(x - hi); then y = (0 + W hi) + W lo, each term
+ * computed like stride_tc_gemm_residual, so every row is batch invariant. The
+ * part of x below lo is under 2^-16 of |x|. */
+int stride_tc_gemm_f32x(const StrideTcGemmF32xParams* p, void* stream);
 
 /* Replaces stride::tc_embed (src/kernels_tc.h:79, src/kernels_tc.cu:179-203):
  * h tile row of lane j <- the fp32 widening of embedding row tokens[j]. */

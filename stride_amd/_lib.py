@@ -75,6 +75,10 @@ class TcLmFullParams(C.Structure):  # src/kernels_tc.h:72-77
     _fields_ = [("l", Lanes), ("x", C.c_void_p), ("m", GemmMat), ("logits", C.c_void_p)]
 
 
+class TcGemmF32xParams(C.Structure):  # no reference counterpart (fp32 activations)
+    _fields_ = [("l", Lanes), ("x", C.c_void_p), ("m", GemmMat), ("y", C.c_void_p), ("workspace", C.c_void_p)]
+
+
 class TcEmbedParams(C.Structure):  # src/kernels_tc.h:10-16
     _fields_ = [("l", Lanes), ("embed", C.c_void_p), ("tokens", C.c_void_p), ("h", C.c_void_p), ("dim", C.c_int32)]
 
@@ -119,6 +123,7 @@ EXPORTS = (
     "stride_tc_mlp13",
     "stride_tc_lm_greedy",
     "stride_tc_lm_full",
+    "stride_tc_gemm_f32x",
     "stride_tc_embed",
     "stride_tc_norm",
     "stride_tc_attention",
@@ -145,6 +150,7 @@ def check_layout() -> None:
     assert C.sizeof(TcMlp13Params) == 64
     assert C.sizeof(TcLmGreedyParams) == 56
     assert C.sizeof(TcLmFullParams) == 48
+    assert C.sizeof(TcGemmF32xParams) == 56
     assert C.sizeof(TcEmbedParams) == 48 and C.sizeof(TcNormParams) == 48 and C.sizeof(TcCompactParams) == 48
     assert AttentionParams.kv.offset == 48 and C.sizeof(AttentionParams) == 176
 
@@ -174,12 +180,13 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     lib.stride_tc_mlp13.argtypes = [C.POINTER(TcMlp13Params), C.c_int, C.c_int, vp]
     lib.stride_tc_lm_greedy.argtypes = [C.POINTER(TcLmGreedyParams), C.c_int, C.c_int, vp]
     lib.stride_tc_lm_full.argtypes = [C.POINTER(TcLmFullParams), C.c_int, vp]
+    lib.stride_tc_gemm_f32x.argtypes = [C.POINTER(TcGemmF32xParams), vp]
     lib.stride_tc_embed.argtypes = [C.POINTER(TcEmbedParams), vp]
     lib.stride_tc_norm.argtypes = [C.POINTER(TcNormParams), C.c_int, vp]
     lib.stride_tc_attention.argtypes = [C.POINTER(AttentionParams), vp]
     lib.stride_tc_compact.argtypes = [C.POINTER(TcCompactParams), vp]
     for name in ("stride_tc_qkv", "stride_tc_gemm_residual", "stride_tc_mlp13", "stride_tc_lm_greedy",
-                 "stride_tc_lm_full", "stride_tc_embed", "stride_tc_norm", "stride_tc_attention", "stride_tc_compact",
+                 "stride_tc_lm_full", "stride_tc_gemm_f32x", "stride_tc_embed", "stride_tc_norm", "stride_tc_attention", "stride_tc_compact",
                  "stride_tc_split_count"):
         getattr(lib, name).restype = C.c_int
     lib.stride_tc_split_count.argtypes = [C.c_int32, C.c_int32]

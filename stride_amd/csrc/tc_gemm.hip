@@ -524,6 +524,41 @@ int run(Geometry g, const typename Epi::Out& o_in, hipStream_t st) {
   return 0;
 }
 
+// fp32 activations rows [rows][cols] -> two bf16 lane-tile sets, hi = bf16(x) and
+// lo = bf16(x - hi), both round to nearest even; lanes past `rows` are zero.
+// Thread i converts 8 consecutive columns of one lane.
+__global__ __launch_bounds__(256) void k_split_f32x(const float* x, int rows, int cols, int lane_groups, uint16_t* hi,
+                                                    uint16_t* lo) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int per_lane = cols / 8;
+  if (i >= static_cast<int64_t>(lane_groups) * 16 * per_lane) return;
+  const int lane = static_cast<int>(i / per_lane), c8 = static_cast<int>(i % per_lane) * 8;
+  uint32_t h[4] = {0u, 0u, 0u, 0u}, l[4] = {0u, 0u, 0u, 0u};
+  if (lane < rows) {
+    const f32x4* src = reinterpret_cast<const f32x4*>(x + static_cast<int64_t>(lane) * cols + c8);
+    const f32x4 a = src[0], b = src[1];
+    const float v[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t hb = bf16_rne(v[k]);
+      const uint32_t lb = bf16_rne(v[k] - f32_of(hb << 16));
+      h[k / 2] |= hb << (16 * (k & 1));
+      l[k / 2] |= lb << (16 * (k & 1));
+    }
+  }
+  // lane tile layout [lt][ct][16 lanes][16 cols]
+  const int64_t at = (static_cast<int64_t>(lane >> 4) * (cols / 16) + c8 / 16) * kTileElems + (lane & 15) * 16 + (c8 & 15);
+  *reinterpret_cast<u32x4*>(hi + at) = u32x4{h[0], h[1], h[2], h[3]};
+  *reinterpret_cast<u32x4*>(lo + at) = u32x4{l[0], l[1], l[2], l[3]};
+}
+
+// Zero-fill of fp32 output (a kernel, so a captured graph holds no memset node).
+__global__ __launch_bounds__(256) void k_zero_f32(float* y, int64_t n) {
+  const int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 4;
+  if (i + 3 < n) *reinterpret_cast<f32x4*>(y + i) = f32x4{0.f, 0.f, 0.f, 0.f};
+  else for (int64_t k = i; k < n; ++k) y[k] = 0.f;
+}
+
 Geometry single(const StrideLanes& l, const uint16_t* x, const StrideGemmMat& m, const uint16_t* w2) {
   Geometry g{};
   g.x = x;
@@ -603,6 +638,28 @@ int stride_tc_gemm_residual(const StrideTcGemmResidualParams* p, int, int, void*
   Geometry g = single(p->l, p->x, p->m, nullptr);
   EpiResidual::Out o{p->h, p->m.groups};
   return run<EpiResidual>(g, o, static_cast<hipStream_t>(stream));
+}
+
+int stride_tc_gemm_f32x(const StrideTcGemmF32xParams* p, void* stream) {
+  std::string why;
+  if (!p) return fail(STRIDE_TC_EINVAL, "gemm_f32x: null params");
+  if (!lanes_ok(p->l, why) || !mat_ok(p->m, "gemm_f32x.m", why)) return fail(STRIDE_TC_EINVAL, "gemm_f32x: " + why);
+  if (!p->x || !p->y || !p->workspace) return fail(STRIDE_TC_EINVAL, "gemm_f32x: null x, y or workspace");
+  if (p->l.rows == 0) return 0;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t lane_elems = static_cast<int64_t>(p->l.lane_groups) * 16 * p->m.cols;
+  uint16_t* hi = p->workspace;
+  uint16_t* lo = p->workspace + lane_elems;
+  const int64_t pieces = static_cast<int64_t>(p->l.lane_groups) * 16 * (p->m.cols / 8);
+  hipLaunchKernelGGL(k_split_f32x, dim3(static_cast<unsigned>((pieces + 255) / 256)), dim3(256), 0, st, p->x, p->l.rows,
+                     p->m.cols, p->l.lane_groups, hi, lo);
+  const int64_t y_elems = static_cast<int64_t>(p->l.lane_groups) * p->m.groups * kTileElems;
+  hipLaunchKernelGGL(k_zero_f32, dim3(static_cast<unsigned>((y_elems / 4 + 255) / 256)), dim3(256), 0, st, p->y, y_elems);
+  if (hipError_t e = hipGetLastError(); e != hipSuccess)
+    return fail(static_cast<int>(e), std::string("gemm_f32x: launch failed: ") + hipGetErrorString(e));
+  EpiResidual::Out o{p->y, p->m.groups};
+  if (int rc = run<EpiResidual>(single(p->l, hi, p->m, nullptr), o, st)) return rc;
+  return run<EpiResidual>(single(p->l, lo, p->m, nullptr), o, st);
 }
 
 int stride_tc_mlp13(const StrideTcMlp13Params* p, int, int, void* stream) {

@@ -121,6 +121,20 @@ class PagedKv:
         self.arena[idx.reshape(-1)] = dense.reshape(-1).to(dev)
 
 
+def gemm_f32x(w_tiles, x_f32, rows: int, y_out=None, workspace=None):
+    """y tiles (h layout, fp32) = W x for row-major fp32 activations x [rows][K]."""
+    lt = (rows + 15) // 16
+    k = int(w_tiles.shape[1]) * 16
+    dev = x_f32.device
+    if y_out is None:
+        y_out = torch.empty((lt, w_tiles.shape[0], 16, 16), dtype=torch.float32, device=dev)
+    if workspace is None:
+        workspace = torch.empty(2 * lt * 16 * k, dtype=U16, device=dev)
+    p = tc.TcGemmF32xParams(lanes(rows), ptr(x_f32), mat(w_tiles), ptr(y_out), ptr(workspace))
+    tc.tc_gemm_f32x(p)
+    return y_out
+
+
 def embed(emb_tiles, tokens, rows: int, dim: int, h_out=None):
     """tc_embed: lane j of fp32 h tiles <- embedding row tokens[j]."""
     lt = (rows + 15) // 16

@@ -24,13 +24,13 @@ import ctypes as C
 
 from . import _lib
 from ._lib import (AttentionParams, BestEntry, GemmMat, KvRef, Lanes, StrideTcError, TcCompactParams, TcEmbedParams,
-                   TcGemmResidualParams, TcLmFullParams, TcLmGreedyParams, TcMlp13Params, TcNormParams, TcQkvParams)
+                   TcGemmF32xParams, TcGemmResidualParams, TcLmFullParams, TcLmGreedyParams, TcMlp13Params, TcNormParams, TcQkvParams)
 
 __all__ = [
     "BestEntry", "GemmMat", "KvRef", "Lanes", "StrideTcError", "TcGemmResidualParams", "TcLmFullParams",
     "TcLmGreedyParams", "TcMlp13Params", "TcQkvParams", "tc_qkv", "tc_gemm_residual", "tc_mlp13", "tc_lm_greedy",
     "tc_lm_full", "kernel_stream", "set_kernel_stream", "mat", "lanes", "ptr", "split_count", "AttentionParams",
-    "TcCompactParams", "TcEmbedParams", "TcNormParams", "tc_embed", "tc_norm", "tc_attention", "tc_compact",
+    "TcCompactParams", "TcEmbedParams", "TcNormParams", "TcGemmF32xParams", "tc_gemm_f32x", "tc_embed", "tc_norm", "tc_attention", "tc_compact",
 ]
 
 _stream = None  # None -> torch's current stream at call time
@@ -110,3 +110,8 @@ def tc_attention(p: AttentionParams) -> None:
 
 def tc_compact(p: TcCompactParams) -> None:
     _lib.check(_lib_().stride_tc_compact(C.byref(p), kernel_stream()))
+
+
+def tc_gemm_f32x(p: TcGemmF32xParams) -> None:
+    """y = W x for fp32 activations (no reference counterpart; see include/stride_tc.h)."""
+    _lib.check(_lib_().stride_tc_gemm_f32x(C.byref(p), kernel_stream()))

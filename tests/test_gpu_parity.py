@@ -60,6 +60,39 @@ def test_config1_projection(exact, m):
     assert np.all(err <= tol_matrix(x, w)), f"max err {err.max()}"
 
 
+@pytest.mark.parametrize("m", [1, 37])
+def test_config1_projection_fp32_x(exact, m):
+    """Config 1 as BASELINE states it: x fp32 ~N(0,1) (not bf16-representable),
+    y = x W^T, N=K=2048, seed 0, through stride_tc_gemm_f32x, against the CPU exact
+    path on the same fp32 x; the rows must not depend on M."""
+    n = k = 2048
+    w = synth.bf16_normal(0, Ids.WO, n, k, 0.02)
+    x = synth.f32_normal(0, Ids.X, m, k)
+    say("config1 fp32 x", m)
+    yt = harness.gemm_f32x(dev_u16(layout.pack_tiles(w)), dev_f32(x), m)
+    torch.cuda.synchronize()
+    y = layout.untile_lanes(yt.cpu().numpy(), m)
+    ref = exact.gemm(w, x)
+    err = np.abs(y.astype(np.float64) - ref)
+    assert np.all(err <= tol_matrix(x, w)), f"max err {err.max()}"
+    y1 = layout.untile_lanes(harness.gemm_f32x(dev_u16(layout.pack_tiles(w)), dev_f32(x[-1:]), 1).cpu().numpy(), 1)
+    assert np.array_equal(y1.view(np.uint32), y[-1:].view(np.uint32))
+
+
+def test_config1_bf16_rounding_alone_fails_the_bound(exact):
+    """Why the fp32-x entry point exists: rounding fp32 x to bf16 before the
+    bf16 GEMM exceeds the tolerance on this input."""
+    n = k = 2048
+    w = synth.bf16_normal(0, Ids.WO, n, k, 0.02)
+    x = synth.f32_normal(0, Ids.X, 1, k)
+    xb = synth.bf16_bits(x)
+    logits = harness.lm_full(dev_u16(layout.pack_tiles(w)), dev_u16(layout.lane_tiles(xb)), 1)
+    torch.cuda.synchronize()
+    y = layout.untile_logits(logits.cpu().numpy(), 1, n)
+    err = np.abs(y.astype(np.float64) - exact.gemm(w, x))
+    assert not np.all(err <= tol_matrix(x, w))
+
+
 @pytest.mark.parametrize("m,n,k", [(1, 256, 2048), (5, 128, 2048), (16, 64, 8192), (17, 256, 2048), (64, 128, 2048),
                                    (130, 128, 1024), (290, 256, 2048), (33, 48, 96)])
 def test_gemm_residual(exact, m, n, k):
