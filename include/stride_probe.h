@@ -32,6 +32,13 @@ int stride_probe_mfma_rate_variant(float* out, int32_t blocks, int32_t iters, in
  * per workgroup to out[blocks]. blocks = 0 picks one workgroup per 64 KiB. */
 int stride_probe_read(const void* buf, int64_t bytes, uint32_t* out, int32_t blocks, int32_t unroll, void* stream);
 
+/* Strip streaming, the decode GEMM pattern: `bytes / strip` strips of `strip`
+ * bytes (a multiple of 1 KiB); wave w of the grid (4 waves per workgroup) reads
+ * strips w, w + waves, ... in 1 KiB pieces (16 bytes per lane), `unroll` (4, 8,
+ * 16) pieces in flight; `rotate` != 0 starts wave w at piece 7w mod pieces. */
+int stride_probe_strip_read(const void* buf, int64_t bytes, int64_t strip, int32_t blocks, int32_t unroll,
+                            int32_t rotate, uint32_t* out, void* stream);
+
 /* Equivalence of the two bf16 MFMA shapes: for each of `cases` 32x32 output
  * blocks chained over `chunks` 32-column chunks from c0, o16 receives the result
  * of v_mfma_f32_16x16x32_bf16 (one per 16x16 sub-block and chunk) and o32 that of

@@ -250,15 +250,19 @@ int stride_tc_split_count(int32_t n, int32_t k);
 /* Tuning hook, no reference counterpart: force the register-streaming kernel
  * configuration `index` (0 .. stride_tc_stream_config_count()-1) for launches of
  * at most 8 lane tiles, or the LDS-pipelined configuration -3-i for every launch
- * it can serve, or -1 for the automatic choice. Every configuration computes
+ * it can serve, or the register-streamed weight / LDS-ring activation
+ * configuration 1000+i, or -1 for the automatic choice. Every configuration computes
  * identical bits; this only changes speed. A configuration that cannot serve a
  * launch is ignored for it. */
 int stride_tc_set_stream_config(int32_t index);
 int stride_tc_stream_config_count(void);
 /* Number of LDS-pipelined configurations (selected as -3-i above). */
 int stride_tc_pipe_config_count(void);
-/* Configuration used by the last launch in this process (-2: the prefill
- * kernel, -1: none yet). */
+/* Number of register-streamed weight / LDS-ring activation configurations
+ * (selected as 1000+i above). */
+int stride_tc_dec_config_count(void);
+/* Configuration used by the last launch in this process, in the numbering of
+ * stride_tc_set_stream_config (-2: the fallback tile kernel, -1: none yet). */
 int stride_tc_last_stream_config(void);
 /* Writes (R, LT, WS, WR, U, flags) of configuration `index` into out6; flags bit 0:
  * activations staged in LDS, bit 1: one K split per workgroup (the last workgroup

@@ -134,6 +134,7 @@ EXPORTS = (
     "stride_tc_set_stream_config",
     "stride_tc_stream_config_count",
     "stride_tc_pipe_config_count",
+    "stride_tc_dec_config_count",
     "stride_tc_stream_config",
     "stride_tc_last_stream_config",
 )
@@ -196,6 +197,8 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     lib.stride_tc_stream_config_count.restype = C.c_int
     lib.stride_tc_pipe_config_count.argtypes = []
     lib.stride_tc_pipe_config_count.restype = C.c_int
+    lib.stride_tc_dec_config_count.argtypes = []
+    lib.stride_tc_dec_config_count.restype = C.c_int
     lib.stride_tc_stream_config.argtypes = [C.c_int32, C.POINTER(C.c_int32)]
     lib.stride_tc_stream_config.restype = C.c_int
     lib.stride_tc_last_stream_config.argtypes = []
@@ -225,6 +228,15 @@ def split_count(n: int, k: int) -> int:
 def pipe_config_count() -> int:
     """Number of LDS-pipelined kernel configurations (forced as -3 - i)."""
     return load().stride_tc_pipe_config_count()
+
+
+DEC_CONFIG_BASE = 1000
+
+
+def dec_config_count() -> int:
+    """Configurations of the register-streamed weight / LDS-ring activation
+    kernel, selected with set_stream_config(DEC_CONFIG_BASE + i)."""
+    return load().stride_tc_dec_config_count()
 
 
 def stream_configs():

@@ -105,6 +105,39 @@ __global__ __launch_bounds__(256) void k_mfma_rate32(float* out, int iters) {
   if (s == 12345.0f) out[threadIdx.x] = s;
 }
 
+
+// Strip streaming: wave w of the grid reads strips w, w + waves, ... of
+// `strip` bytes each, one 1 KiB piece (16 bytes per lane) per load, U pieces in
+// flight; the pattern of the decode GEMMs, where every wave streams one row
+// tile's contiguous K strip. With `rotate`, wave w starts its strip at piece
+// (w * 7) mod pieces and wraps, so that waves in lockstep touch different
+// offsets at any moment.
+template <int U>
+__global__ __launch_bounds__(256) void k_strip_read(const char* buf, int64_t nstrips, int64_t strip, int rotate,
+                                                    uint32_t* out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int64_t waves = static_cast<int64_t>(gridDim.x) * 4;
+  const int pieces = static_cast<int>(strip / 1024);
+  uint32_t x = 0;
+  for (int64_t sidx = wave; sidx < nstrips; sidx += waves) {
+    const char* base = buf + sidx * strip + lane * 16;
+    const int r0 = rotate ? static_cast<int>((wave * 7) % pieces) : 0;
+    for (int p = 0; p + U <= pieces; p += U) {
+      u32x4 v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        int q = r0 + p + u;
+        q = q >= pieces ? q - pieces : q;
+        v[u] = load16(base + static_cast<int64_t>(q) * 1024);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) x ^= v[u][0] ^ v[u][1] ^ v[u][2] ^ v[u][3];
+    }
+  }
+  if (x == 0x12345678u) out[0] = x;
+}
+
 }  // namespace
 
 extern "C" int stride_probe_mfma_rate_variant(float* out, int32_t blocks, int32_t iters, int32_t variant, void* stream) {
@@ -197,5 +230,20 @@ extern "C" int stride_probe_mfma_equiv(const uint16_t* a, const uint16_t* b, con
                                        int32_t cases, int32_t chunks, void* stream) {
   if (cases <= 0 || chunks <= 0) return 1;
   hipLaunchKernelGGL(k_mfma_equiv, dim3(cases), dim3(64), 0, static_cast<hipStream_t>(stream), a, b, c0, o16, o32, chunks);
+  return static_cast<int>(hipGetLastError());
+}
+
+extern "C" int stride_probe_strip_read(const void* buf, int64_t bytes, int64_t strip, int32_t blocks, int32_t unroll,
+                                       int32_t rotate, uint32_t* out, void* stream) {
+  if (!buf || !out || strip < 1024 || strip % 1024 != 0 || bytes < strip || blocks <= 0) return 1;
+  const int64_t nstrips = bytes / strip;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const char* p = static_cast<const char*>(buf);
+  switch (unroll) {
+    case 4: hipLaunchKernelGGL(k_strip_read<4>, dim3(blocks), dim3(256), 0, st, p, nstrips, strip, rotate, out); break;
+    case 8: hipLaunchKernelGGL(k_strip_read<8>, dim3(blocks), dim3(256), 0, st, p, nstrips, strip, rotate, out); break;
+    case 16: hipLaunchKernelGGL(k_strip_read<16>, dim3(blocks), dim3(256), 0, st, p, nstrips, strip, rotate, out); break;
+    default: return 1;
+  }
   return static_cast<int>(hipGetLastError());
 }

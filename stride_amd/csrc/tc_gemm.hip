@@ -39,6 +39,7 @@
 #include <cstring>
 #include <string>
 
+#include "tc_dec.hpp"
 #include "tc_epilogue.hpp"
 #include "tc_pipe.hpp"
 #include "tc_stream.hpp"
@@ -268,6 +269,90 @@ bool decode_cfg_fits(const DecodeCfg& c, Geometry g, int smax, int mats, bool re
   return true;
 }
 
+// Configurations of k_dec (weights to registers, activations through an LDS
+// ring): (R row tiles per wave, LT lane tiles, NW waves, KC chunks per stage,
+// NSS ring slots, XS one split per workgroup, WS split groups per workgroup). Index 1000 + i in the tuning hook
+// selects configuration i.
+#define STRIDE_TC_DEC_CONFIGS(D)    \
+  D(0, 1, 8, 4, 2, 4, true, 1)     \
+  D(1, 1, 8, 4, 1, 8, true, 1)     \
+  D(2, 1, 8, 8, 2, 4, true, 1)     \
+  D(3, 1, 8, 4, 2, 4, false, 2)    \
+  D(4, 1, 8, 4, 2, 4, false, 1)    \
+  D(5, 2, 8, 4, 2, 4, false, 1)    \
+  D(6, 1, 4, 4, 2, 4, true, 1)     \
+  D(7, 1, 4, 4, 1, 8, true, 1)     \
+  D(8, 2, 4, 4, 2, 4, false, 1)    \
+  D(9, 1, 8, 4, 1, 8, false, 2)    \
+  D(10, 1, 4, 4, 2, 4, false, 1)   \
+  D(11, 1, 4, 4, 2, 4, false, 2)   \
+  D(12, 1, 8, 2, 2, 4, false, 2)   \
+  D(13, 1, 4, 4, 1, 8, false, 2)   \
+  D(14, 2, 8, 4, 1, 8, false, 1)   \
+  D(15, 1, 2, 2, 2, 4, true, 1)
+
+struct DecCfg {
+  int r, lt, nw, kc, nss;
+  bool xs;
+  int ws;
+};
+#define STRIDE_TC_DEC_ROW(i, R, LT, NW, KC, NSS, XS, WS) {R, LT, NW, KC, NSS, XS, WS},
+constexpr DecCfg kDecCfgs[] = {STRIDE_TC_DEC_CONFIGS(STRIDE_TC_DEC_ROW)};
+#undef STRIDE_TC_DEC_ROW
+constexpr int kNumDecCfgs = sizeof(kDecCfgs) / sizeof(kDecCfgs[0]);
+constexpr int kDecIndexBase = 1000;
+int g_forced_dec = -1;
+
+bool dec_cfg_fits(const DecCfg& c, const Geometry& g, int smax, int mats, bool reduce) {
+  const int chunks = g.col_tiles >> 1;
+  if (c.xs) {
+    if (reduce || smax < 2 || smax > kMaxXSplits) return false;
+    if (total_tiles(g) * smax * mats * 1024 > kScratchBytes) return false;
+    int64_t units = 0;
+    for (int i = 0; i < g.nseg; ++i) units += (g.seg[i].row_tiles + c.nw * c.r - 1) / (c.nw * c.r);
+    if (units * ((g.lane_groups + c.lt - 1) / c.lt) > kSplitUnits) return false;
+  } else {
+    if (reduce && c.ws != 1) return false;
+    for (int i = 0; i < g.nseg; ++i)
+      if (g.seg[i].splits != c.ws) return false;
+  }
+  for (int i = 0; i < g.nseg; ++i) {
+    const int per = chunks / g.seg[i].splits;
+    if (per % c.kc != 0 || (per / c.kc) % c.nss != 0) return false;
+  }
+  return true;
+}
+
+template <class Epi, int R, int LT, int NW, int KC, int NSS, bool XS, int WS>
+void launch_dec(Geometry g, const typename Epi::Out& o, hipStream_t st) {
+  if constexpr ((XS || WS > 1) && Epi::kReduce) {
+    return;  // never selected (dec_cfg_fits)
+  } else {
+    constexpr int NR = NW / WS;
+    int blocks = 0;
+    for (int i = 0; i < g.nseg; ++i) {
+      g.seg[i].blocks = (g.seg[i].row_tiles + NR * R - 1) / (NR * R);
+      blocks += XS ? g.seg[i].blocks * g.seg[i].splits : g.seg[i].blocks;
+    }
+    blocks *= (g.lane_groups + LT - 1) / LT;
+    hipLaunchKernelGGL((k_dec<Epi, R, LT, NW, KC, NSS, XS, WS>), dim3(blocks), dim3(kWave * NW), 0, st, g, o);
+  }
+}
+
+template <class Epi>
+void launch_dec_cfg(int idx, const Geometry& g, const typename Epi::Out& o, hipStream_t st) {
+  switch (idx) {
+#define STRIDE_TC_DEC_CASE(i, R, LT, NW, KC, NSS, XS, WS) \
+  case i:                                                  \
+    launch_dec<Epi, R, LT, NW, KC, NSS, XS, WS>(g, o, st); \
+    break;
+    STRIDE_TC_DEC_CONFIGS(STRIDE_TC_DEC_CASE)
+#undef STRIDE_TC_DEC_CASE
+    default:
+      break;
+  }
+}
+
 // Default choice by lane-tile count, split count, segment count and split
 // length, from measured sweeps on MI355X (HIP-graph timing, weights rotated past
 // the MALL).
@@ -406,16 +491,22 @@ int pipe_rows_per_block(int idx, int mats) {
 
 // Automatic choice of kernel family and configuration, from measured sweeps on
 // MI355X (HIP-graph timing, weights rotated past the MALL; every choice computes
-// the same bits). kind 0: k_stream configuration, kind 1: k_pipe configuration.
+// the same bits). kind 0: k_stream configuration, kind 1: k_pipe configuration,
+// kind 3: k_dec configuration.
 struct Pick {
   int kind, idx;
 };
 
-// At most 8 lane tiles. The LDS-pipelined kernel with small blocks wins for the
-// LM head from two lane tiles up and for the paired gate/up GEMM from three.
+// At most 8 lane tiles. At three or four lane tiles the register-streamed
+// kernel with an activation ring wins for the LM head and (two split groups per
+// workgroup) for the paired gate/up GEMM; otherwise the LDS-pipelined kernel
+// with small blocks wins for the LM head from two lane tiles up and for gate/up
+// from three.
 Pick pick_small(int T, int smax, int mats, int nseg, int per) {
+  if (smax == 1 && T >= 3 && T <= 4) return {3, 8};
   if (smax == 1 && T >= 2) return {1, T <= 4 ? 14 : 8};
-  if (smax == 2 && mats == 2 && T >= 3) return {1, T <= 4 ? 17 : 15};
+  if (smax == 2 && mats == 2 && T >= 3 && T <= 4) return {3, 13};
+  if (smax == 2 && mats == 2 && T >= 3) return {1, 15};
   return {0, pick_decode(T, smax, mats, nseg, per)};
 }
 
@@ -461,12 +552,17 @@ int run(Geometry g, const typename Epi::Out& o_in, hipStream_t st) {
     smax = g.seg[i].splits > smax ? g.seg[i].splits : smax;
   }
   const int T = g.lane_groups;
-  int kind = 0, idx = 0, rows_per_block = 0;  // kind 0: streaming, 1: pipe, 2: legacy tile
+  int kind = 0, idx = 0, rows_per_block = 0;  // kind 0: streaming, 1: pipe, 2: legacy tile, 3: dec
   const int per = (g.col_tiles >> 1) / smax;
   const bool forced_stream =
       g_forced_cfg >= 0 && decode_cfg_fits(kDecodeCfgs[g_forced_cfg], g, smax, Epi::kMats, Epi::kReduce);
   const bool forced_pipe = g_forced_pipe >= 0 && pipe_cfg_fits(g_forced_pipe, g);
-  if (forced_stream) {
+  const bool forced_dec =
+      g_forced_dec >= 0 && dec_cfg_fits(kDecCfgs[g_forced_dec], g, smax, Epi::kMats, Epi::kReduce);
+  if (forced_dec) {
+    kind = 3;
+    idx = g_forced_dec;
+  } else if (forced_stream) {
     idx = g_forced_cfg;
   } else if (forced_pipe) {
     kind = 1;
@@ -480,6 +576,10 @@ int run(Geometry g, const typename Epi::Out& o_in, hipStream_t st) {
       if (!pipe_cfg_fits(idx, g)) idx = 0;
       if (!pipe_cfg_fits(idx, g)) kind = 2;
     }
+    if (kind == 3 && !dec_cfg_fits(kDecCfgs[idx], g, smax, Epi::kMats, Epi::kReduce)) {
+      kind = 0;
+      idx = pick_decode(T, smax, Epi::kMats, g.nseg, per);
+    }
     if (kind == 0 && !decode_cfg_fits(kDecodeCfgs[idx], g, smax, Epi::kMats, Epi::kReduce)) {
       // a register-only in-workgroup configuration with a wave per split always fits
       idx = smax == 1 ? 3 : (smax == 2 ? 2 : (smax <= 8 ? 0 : 18));
@@ -487,6 +587,7 @@ int run(Geometry g, const typename Epi::Out& o_in, hipStream_t st) {
   }
   if (kind == 0) rows_per_block = kDecodeCfgs[idx].wr * kDecodeCfgs[idx].r;
   if (kind == 1) rows_per_block = pipe_rows_per_block(idx, Epi::kMats);
+  if (kind == 3) rows_per_block = kDecCfgs[idx].nw / kDecCfgs[idx].ws * kDecCfgs[idx].r;
   // Greedy LM head: two passes through the candidate scratch when it fits.
   int nrb = 0;
   if constexpr (Epi::kReduce) {
@@ -508,6 +609,15 @@ int run(Geometry g, const typename Epi::Out& o_in, hipStream_t st) {
       if (!g.part || !g.split_cnt) return fail(STRIDE_TC_EINVAL, "split scratch unavailable");
     }
     launch_decode_cfg<Epi>(idx, g, o, st);
+  } else if (kind == 3) {
+    g_last_cfg = kDecIndexBase + idx;
+    if (kDecCfgs[idx].xs) {
+      g.part = reinterpret_cast<float*>(scratch_base());
+      g.split_cnt = split_counters();
+      g.part_splits = smax;
+      if (!g.part || !g.split_cnt) return fail(STRIDE_TC_EINVAL, "split scratch unavailable");
+    }
+    launch_dec_cfg<Epi>(idx, g, o, st);
   } else if (kind == 1) {
     g_last_cfg = -3 - idx;
     launch_pipe_cfg<Epi>(idx, g, o, smax, st);
@@ -594,14 +704,21 @@ extern "C" {
 int stride_tc_set_stream_config(int32_t index) {
   if (index <= -3 && -3 - index < kNumPipeCfgs) {
     g_forced_pipe = -3 - index;
-    g_forced_cfg = -1;
+    g_forced_cfg = g_forced_dec = -1;
+    return 0;
+  }
+  if (index >= kDecIndexBase && index - kDecIndexBase < kNumDecCfgs) {
+    g_forced_dec = index - kDecIndexBase;
+    g_forced_cfg = g_forced_pipe = -1;
     return 0;
   }
   if (index < -1 || index >= kNumDecodeCfgs) return fail(STRIDE_TC_EINVAL, "config index out of range");
   g_forced_cfg = index;
-  g_forced_pipe = -1;
+  g_forced_pipe = g_forced_dec = -1;
   return 0;
 }
+
+int stride_tc_dec_config_count(void) { return kNumDecCfgs; }
 
 int stride_tc_stream_config_count(void) { return kNumDecodeCfgs; }
 

@@ -23,6 +23,119 @@ namespace stride_tc {
 // Largest split count served by cross-workgroup split launches (XS).
 constexpr int kMaxXSplits = 8;
 
+// Output-tile and unit bases of segment si for the cross-workgroup split scratch.
+__device__ __forceinline__ int xs_tile0(const Geometry& g, int si) {
+  int t = 0;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+    if (i < si) t += g.seg[i].row_tiles * g.lane_groups;
+  return t;
+}
+__device__ __forceinline__ int xs_unit0(const Geometry& g, int si) {
+  int u = 0;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+    if (i < si) u += g.seg[i].blocks;
+  return u;
+}
+
+// Finish of a cross-workgroup split launch (one split per workgroup). With a
+// single split the tiles are final. Otherwise every workgroup of a (row block,
+// lane group) unit publishes its partial tiles with device-coherent stores and
+// counts itself in at `cnt`; the last one to arrive folds the splits in
+// ascending order, y = ((c0 + c1) + c2) + ..., applies the epilogue and re-arms
+// the counter for the next launch. Nothing waits on another workgroup. Rows
+// rt_first .. rt_first+R-1 and lane tiles lt0 .. lt0+nlt-1 are this wave's.
+template <class Epi, int R, int LT>
+__device__ __forceinline__ void xs_finish(const Geometry& g, const typename Epi::Out& o, int si, const Segment& sg,
+                                          int rt_first, int lt0, int nlt, int* cnt, int splits, int my_split,
+                                          const f32x4 (&acc)[Epi::kMats][R][LT], int lane) {
+  constexpr int M = Epi::kMats;
+  if (splits == 1) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if (rt_first + r >= sg.row_tiles) continue;
+#pragma unroll
+      for (int l = 0; l < LT; ++l) {
+        if (l >= nlt) continue;
+        f32x4 y[M];
+#pragma unroll
+        for (int m = 0; m < M; ++m) y[m] = acc[m][r][l];
+        Epi::apply(o, g, si, rt_first + r, lt0 + l, y, lane);
+      }
+    }
+    return;
+  }
+  const int tile0 = xs_tile0(g, si);
+  auto slot = [&](int r, int l, int s, int m) {
+    const int64_t tile = tile0 + static_cast<int64_t>(rt_first + r) * g.lane_groups + lt0 + l;
+    return reinterpret_cast<uint64_t*>(g.part) + ((tile * g.part_splits + s) * M + m) * (2 * kWave) + 2 * lane;
+  };
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    if (rt_first + r >= sg.row_tiles) continue;
+#pragma unroll
+    for (int l = 0; l < LT; ++l) {
+      if (l >= nlt) continue;
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        uint64_t* p = slot(r, l, my_split, m);
+        const f32x4 v = acc[m][r][l];
+        __hip_atomic_store(p, static_cast<uint64_t>(u32_of(v[0])) | (static_cast<uint64_t>(u32_of(v[1])) << 32),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(p + 1, static_cast<uint64_t>(u32_of(v[2])) | (static_cast<uint64_t>(u32_of(v[3])) << 32),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  }
+  // The partial stores are complete (performed at device scope) before this
+  // workgroup is counted.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  __shared__ int last;
+  if (threadIdx.x == 0) {
+    const int before = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last = before == splits - 1;
+    if (last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!last) return;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    if (rt_first + r >= sg.row_tiles) continue;
+#pragma unroll
+    for (int l = 0; l < LT; ++l) {
+      if (l >= nlt) continue;
+      // Issue every partial load first (at most kMaxXSplits splits, a
+      // wave-uniform bound), then fold in ascending split order.
+      f32x4 part[kMaxXSplits][M];
+#pragma unroll
+      for (int s = 0; s < kMaxXSplits; ++s) {
+        if (s >= splits || s == my_split) continue;
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+          const uint64_t* p = slot(r, l, s, m);
+          const uint64_t lo = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          const uint64_t hi = __hip_atomic_load(p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          part[s][m] = f32x4{f32_of(static_cast<uint32_t>(lo)), f32_of(static_cast<uint32_t>(lo >> 32)),
+                             f32_of(static_cast<uint32_t>(hi)), f32_of(static_cast<uint32_t>(hi >> 32))};
+        }
+      }
+      f32x4 y[M];
+#pragma unroll
+      for (int s = 0; s < kMaxXSplits; ++s) {
+        if (s >= splits) continue;
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+          const f32x4 v = s == my_split ? acc[m][r][l] : part[s][m];
+          y[m] = s == 0 ? v : y[m] + v;
+        }
+      }
+      Epi::apply(o, g, si, rt_first + r, lt0 + l, y, lane);
+    }
+  }
+}
+
 template <class Epi, int R, int LT, int WS, int WR, int UC, bool XLC, bool XS>
 __global__ __launch_bounds__(kWave * WS * WR) void k_stream(Geometry g, typename Epi::Out o) {
   static_assert(!XS || (WS == 1 && !Epi::kReduce), "cross-workgroup splits use one split group and a plain epilogue");
@@ -247,103 +360,8 @@ __global__ __launch_bounds__(kWave * WS * WR) void k_stream(Geometry g, typename
   }
 
   if constexpr (XS) {
-    // One split of each tile. With a single split, finish here. Otherwise every
-    // workgroup of a (row block, lane group) unit publishes its partial tiles
-    // with device-coherent stores and counts itself in; the last one to arrive
-    // folds the splits in ascending order, applies the epilogue and re-arms the
-    // counter for the next launch. Nothing waits on another workgroup.
-    int tile0 = 0, unit0 = 0;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      if (i < si) {
-        tile0 += g.seg[i].row_tiles * g.lane_groups;
-        unit0 += g.seg[i].blocks;
-      }
-    }
-    if (splits == 1) {
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        if (rt_first + r >= sg.row_tiles) continue;
-#pragma unroll
-        for (int l = 0; l < LT; ++l) {
-          if (l >= nlt) continue;
-          f32x4 y[M];
-#pragma unroll
-          for (int m = 0; m < M; ++m) y[m] = acc[m][r][l];
-          Epi::apply(o, g, si, rt_first + r, lt0 + l, y, lane);
-        }
-      }
-    } else {
-      auto slot = [&](int r, int l, int s, int m) {
-        const int64_t tile = tile0 + static_cast<int64_t>(rt_first + r) * g.lane_groups + lt0 + l;
-        return reinterpret_cast<uint64_t*>(g.part) + ((tile * g.part_splits + s) * M + m) * (2 * kWave) + 2 * lane;
-      };
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        if (rt_first + r >= sg.row_tiles) continue;
-#pragma unroll
-        for (int l = 0; l < LT; ++l) {
-          if (l >= nlt) continue;
-#pragma unroll
-          for (int m = 0; m < M; ++m) {
-            uint64_t* p = slot(r, l, my_split, m);
-            const f32x4 v = acc[m][r][l];
-            __hip_atomic_store(p, static_cast<uint64_t>(u32_of(v[0])) | (static_cast<uint64_t>(u32_of(v[1])) << 32),
-                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(p + 1, static_cast<uint64_t>(u32_of(v[2])) | (static_cast<uint64_t>(u32_of(v[3])) << 32),
-                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          }
-        }
-      }
-      // The partial stores are complete (performed at device scope) before this
-      // workgroup is counted.
-      __builtin_amdgcn_s_waitcnt(0);
-      __syncthreads();
-      __shared__ int last;
-      int* cnt = g.split_cnt + static_cast<int64_t>(unit0 + rb) * lgroups + (lt0 / LT);
-      if (threadIdx.x == 0) {
-        const int before = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        last = before == splits - 1;
-        if (last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-      __syncthreads();
-      if (last) {
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-          if (rt_first + r >= sg.row_tiles) continue;
-#pragma unroll
-          for (int l = 0; l < LT; ++l) {
-            if (l >= nlt) continue;
-            // Issue every partial load first (at most kMaxXSplits splits, a
-            // wave-uniform bound), then fold in ascending split order.
-            f32x4 part[kMaxXSplits][M];
-#pragma unroll
-            for (int s = 0; s < kMaxXSplits; ++s) {
-              if (s >= splits || s == my_split) continue;
-#pragma unroll
-              for (int m = 0; m < M; ++m) {
-                const uint64_t* p = slot(r, l, s, m);
-                const uint64_t lo = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                const uint64_t hi = __hip_atomic_load(p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                part[s][m] = f32x4{f32_of(static_cast<uint32_t>(lo)), f32_of(static_cast<uint32_t>(lo >> 32)),
-                                   f32_of(static_cast<uint32_t>(hi)), f32_of(static_cast<uint32_t>(hi >> 32))};
-              }
-            }
-            f32x4 y[M];
-#pragma unroll
-            for (int s = 0; s < kMaxXSplits; ++s) {
-              if (s >= splits) continue;
-#pragma unroll
-              for (int m = 0; m < M; ++m) {
-                const f32x4 v = s == my_split ? acc[m][r][l] : part[s][m];
-                y[m] = s == 0 ? v : y[m] + v;
-              }
-            }
-            Epi::apply(o, g, si, rt_first + r, lt0 + l, y, lane);
-          }
-        }
-      }
-    }
+    int* cnt = g.split_cnt + static_cast<int64_t>(xs_unit0(g, si) + rb) * lgroups + (lt0 / LT);
+    xs_finish<Epi, R, LT>(g, o, si, sg, rt_first, lt0, nlt, cnt, splits, my_split, acc, lane);
   } else if constexpr (Epi::kReduce) {
     // Candidates of every tile this workgroup owns are merged first; then one
     // wave publishes a single update per batch lane.

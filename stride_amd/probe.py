@@ -27,6 +27,8 @@ def load():
         lib.stride_probe_mfma_rate_variant.restype = C.c_int
         lib.stride_probe_mfma_equiv.argtypes = [vp, vp, vp, vp, vp, C.c_int32, C.c_int32, vp]
         lib.stride_probe_mfma_equiv.restype = C.c_int
+        lib.stride_probe_strip_read.argtypes = [vp, C.c_int64, C.c_int64, C.c_int32, C.c_int32, C.c_int32, vp, vp]
+        lib.stride_probe_strip_read.restype = C.c_int
         _lib = lib
     return _lib
 
@@ -42,6 +44,13 @@ def read(buf, out, blocks: int, unroll: int, stream: int) -> None:
                                   stream)
     if rc:
         raise RuntimeError(f"stride_probe_read failed ({rc})")
+
+
+def strip_read(buf, strip: int, out, blocks: int, unroll: int, rotate: int, stream: int) -> None:
+    rc = load().stride_probe_strip_read(buf.data_ptr(), buf.numel() * buf.element_size(), strip, blocks, unroll,
+                                        rotate, out.data_ptr(), stream)
+    if rc:
+        raise RuntimeError(f"stride_probe_strip_read failed ({rc})")
 
 
 def mfma_rate(out, blocks: int, iters: int, stream: int) -> None:

@@ -1,6 +1,7 @@
 """Every decode-regime kernel configuration (in-workgroup split, cross-workgroup
-split, x staged in LDS or not, any register blocking) must produce bit-identical
-outputs: the configuration is a speed choice, never a numerical one."""
+split, x staged in LDS or not, any register blocking, weights streamed to
+registers with activations in an LDS ring) must produce bit-identical outputs:
+the configuration is a speed choice, never a numerical one."""
 import hashlib
 
 import pytest
@@ -28,7 +29,7 @@ def setup():
     def w(n, k, rows=None):
         return layout.pack_tiles((torch.randn(n, k, generator=g, device=DEV) * 0.02).to(torch.bfloat16).view(torch.int16), rows)
 
-    W = dict(o=w(2048, 2048), down=w(512, 8192), w1=w(1024, 2048), w3=w(1024, 2048), lm=w(4000, 2048),
+    W = dict(o=w(2048, 2048), down=w(512, 8192), w1=w(1024, 2048), w3=w(1024, 2048), lm=w(4000, 2048), lm1=w(16400, 2048),
              q=w(512, 2048, layout.rope_rows(512, 64)), k=w(128, 2048, layout.rope_rows(128, 64)),
              v=w(128, 2048, layout.rope_rows(128, 64)))
     x = {k: (torch.randn(128, k, generator=g, device=DEV)).to(torch.bfloat16).view(torch.int16) for k in (2048, 8192)}
@@ -48,6 +49,8 @@ def run_all(W, x, h, m):
     out["down"] = digest(hd)
     out["gate_up"] = digest(harness.mlp13(W["w1"], W["w3"], xt, m))
     out["lm"] = digest(harness.lm_greedy(W["lm"], xt, m, 3990))
+    out["lm1"] = digest(harness.lm_greedy(W["lm1"], xt, m, 16390))  # a single split
+    out["lm1_full"] = digest(harness.lm_full(W["lm1"], xt, m))
     kv = harness.PagedKv.create(m, 16, 2, 64, 1, 16, DEV)
     rope = W["rope"]
     q = harness.qkv(W["q"], W["k"], W["v"], xt, m, 64, rope, torch.arange(m, dtype=torch.int32, device=DEV),
@@ -89,5 +92,21 @@ def test_all_prefill_configs_identical(setup, m):
             got = run_all(W, xx, hh, m)
             for k in ref:
                 assert got[k] == ref[k], f"prefill config {i} changes {k} bits at M={m}"
+    finally:
+        _lib.set_stream_config(-1)
+
+
+@pytest.mark.parametrize("m", [1, 20, 64, 128])
+def test_all_dec_configs_identical(setup, m):
+    W, x, h = setup
+    _lib.set_stream_config(-1)
+    ref = run_all(W, x, h, m)
+    try:
+        for i in range(_lib.dec_config_count()):
+            say("dec config", i, "M =", m)
+            _lib.set_stream_config(_lib.DEC_CONFIG_BASE + i)
+            got = run_all(W, x, h, m)
+            for k in ref:
+                assert got[k] == ref[k], f"dec config {i} changes {k} bits at M={m}"
     finally:
         _lib.set_stream_config(-1)
