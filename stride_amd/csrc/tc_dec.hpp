@@ -37,8 +37,8 @@
 
 namespace stride_tc {
 
-template <class Epi, int R, int LT, int NW, int KC, int NSS, bool XS, int WS>
-__global__ __launch_bounds__(kWave * NW) void k_dec(Geometry g, typename Epi::Out o) {
+template <class Epi, int R, int LT, int NW, int KC, int NSS, bool XS, int WS, int OCC>
+__global__ __launch_bounds__(kWave * NW, OCC) void k_dec(Geometry g, typename Epi::Out o) {
   static_assert(!(XS && Epi::kReduce), "the argmax epilogue needs whole tiles");
   static_assert(NSS >= 2, "at least one stage in flight");
   static_assert(NW % WS == 0 && (!XS || WS == 1), "split groups divide the waves; XS runs one split");

@@ -271,32 +271,39 @@ bool decode_cfg_fits(const DecodeCfg& c, Geometry g, int smax, int mats, bool re
 
 // Configurations of k_dec (weights to registers, activations through an LDS
 // ring): (R row tiles per wave, LT lane tiles, NW waves, KC chunks per stage,
-// NSS ring slots, XS one split per workgroup, WS split groups per workgroup). Index 1000 + i in the tuning hook
+// NSS ring slots, XS one split per workgroup, WS split groups per workgroup, OCC
+// workgroups per CU the register allocation is bounded for). Index 1000 + i in the tuning hook
 // selects configuration i.
-#define STRIDE_TC_DEC_CONFIGS(D)    \
-  D(0, 1, 8, 4, 2, 4, true, 1)     \
-  D(1, 1, 8, 4, 1, 8, true, 1)     \
-  D(2, 1, 8, 8, 2, 4, true, 1)     \
-  D(3, 1, 8, 4, 2, 4, false, 2)    \
-  D(4, 1, 8, 4, 2, 4, false, 1)    \
-  D(5, 2, 8, 4, 2, 4, false, 1)    \
-  D(6, 1, 4, 4, 2, 4, true, 1)     \
-  D(7, 1, 4, 4, 1, 8, true, 1)     \
-  D(8, 2, 4, 4, 2, 4, false, 1)    \
-  D(9, 1, 8, 4, 1, 8, false, 2)    \
-  D(10, 1, 4, 4, 2, 4, false, 1)   \
-  D(11, 1, 4, 4, 2, 4, false, 2)   \
-  D(12, 1, 8, 2, 2, 4, false, 2)   \
-  D(13, 1, 4, 4, 1, 8, false, 2)   \
-  D(14, 2, 8, 4, 1, 8, false, 1)   \
-  D(15, 1, 2, 2, 2, 4, true, 1)
+#define STRIDE_TC_DEC_CONFIGS(D)       \
+  D(0, 1, 8, 4, 2, 4, true, 1, 1)     \
+  D(1, 1, 8, 4, 1, 8, true, 1, 1)     \
+  D(2, 1, 8, 8, 2, 4, true, 1, 1)     \
+  D(3, 1, 8, 4, 2, 4, false, 2, 1)    \
+  D(4, 1, 8, 4, 2, 4, false, 1, 1)    \
+  D(5, 2, 8, 4, 2, 4, false, 1, 1)    \
+  D(6, 1, 4, 4, 2, 4, true, 1, 1)     \
+  D(7, 1, 4, 4, 1, 8, true, 1, 1)     \
+  D(8, 2, 4, 4, 2, 4, false, 1, 1)    \
+  D(9, 1, 8, 4, 1, 8, false, 2, 1)    \
+  D(10, 1, 4, 4, 2, 4, false, 1, 1)   \
+  D(11, 1, 4, 4, 2, 4, false, 2, 1)   \
+  D(12, 2, 8, 4, 1, 4, false, 1, 2)   \
+  D(13, 1, 4, 4, 1, 8, false, 2, 1)   \
+  D(14, 2, 8, 4, 1, 8, false, 1, 1)   \
+  D(15, 1, 2, 2, 2, 4, true, 1, 1)    \
+  D(16, 1, 8, 4, 1, 4, false, 1, 2)   \
+  D(17, 2, 8, 4, 1, 6, false, 1, 2)   \
+  D(18, 2, 4, 4, 2, 4, false, 1, 2)   \
+  D(19, 4, 4, 4, 1, 4, false, 1, 2)   \
+  D(20, 1, 8, 4, 1, 4, false, 2, 2)   \
+  D(21, 2, 8, 8, 1, 4, false, 1, 1)
 
 struct DecCfg {
   int r, lt, nw, kc, nss;
   bool xs;
-  int ws;
+  int ws, occ;
 };
-#define STRIDE_TC_DEC_ROW(i, R, LT, NW, KC, NSS, XS, WS) {R, LT, NW, KC, NSS, XS, WS},
+#define STRIDE_TC_DEC_ROW(i, R, LT, NW, KC, NSS, XS, WS, OCC) {R, LT, NW, KC, NSS, XS, WS, OCC},
 constexpr DecCfg kDecCfgs[] = {STRIDE_TC_DEC_CONFIGS(STRIDE_TC_DEC_ROW)};
 #undef STRIDE_TC_DEC_ROW
 constexpr int kNumDecCfgs = sizeof(kDecCfgs) / sizeof(kDecCfgs[0]);
@@ -323,7 +330,7 @@ bool dec_cfg_fits(const DecCfg& c, const Geometry& g, int smax, int mats, bool r
   return true;
 }
 
-template <class Epi, int R, int LT, int NW, int KC, int NSS, bool XS, int WS>
+template <class Epi, int R, int LT, int NW, int KC, int NSS, bool XS, int WS, int OCC>
 void launch_dec(Geometry g, const typename Epi::Out& o, hipStream_t st) {
   if constexpr ((XS || WS > 1) && Epi::kReduce) {
     return;  // never selected (dec_cfg_fits)
@@ -335,16 +342,16 @@ void launch_dec(Geometry g, const typename Epi::Out& o, hipStream_t st) {
       blocks += XS ? g.seg[i].blocks * g.seg[i].splits : g.seg[i].blocks;
     }
     blocks *= (g.lane_groups + LT - 1) / LT;
-    hipLaunchKernelGGL((k_dec<Epi, R, LT, NW, KC, NSS, XS, WS>), dim3(blocks), dim3(kWave * NW), 0, st, g, o);
+    hipLaunchKernelGGL((k_dec<Epi, R, LT, NW, KC, NSS, XS, WS, OCC>), dim3(blocks), dim3(kWave * NW), 0, st, g, o);
   }
 }
 
 template <class Epi>
 void launch_dec_cfg(int idx, const Geometry& g, const typename Epi::Out& o, hipStream_t st) {
   switch (idx) {
-#define STRIDE_TC_DEC_CASE(i, R, LT, NW, KC, NSS, XS, WS) \
-  case i:                                                  \
-    launch_dec<Epi, R, LT, NW, KC, NSS, XS, WS>(g, o, st); \
+#define STRIDE_TC_DEC_CASE(i, R, LT, NW, KC, NSS, XS, WS, OCC) \
+  case i:                                                       \
+    launch_dec<Epi, R, LT, NW, KC, NSS, XS, WS, OCC>(g, o, st); \
     break;
     STRIDE_TC_DEC_CONFIGS(STRIDE_TC_DEC_CASE)
 #undef STRIDE_TC_DEC_CASE
