@@ -15,8 +15,9 @@ Each sequence keeps the reference scheduler's fingerprint (src/scheduler.cpp:
 15-24, 280): FNV-1a over the little-endian bytes of each generated token id and
 of the fp32 bits of its logit, starting from the FNV offset basis.
 
-The weights are random-init Llama-3.2-1B-shaped tiles (no checkpoint is loaded;
-the tile formats are those of the reference's pack_tiles, src/model.cpp:114-226).
+Weights come from stride_amd.weights: a safetensors checkpoint packed as the
+reference's Weights constructor packs it (src/model.cpp:139-238), or random-init
+tiles of the same shapes.
 """
 from __future__ import annotations
 
@@ -27,6 +28,8 @@ import numpy as np
 import torch
 
 from . import harness, layout, tc
+from .weights import ModelConfig
+from .weights import Weights as PackedWeights
 
 FNV_OFFSET = 14695981039346656037
 FNV_PRIME = 1099511628211
@@ -40,50 +43,14 @@ def fnv_mix(h: int, v: int) -> int:
     return h
 
 
-@dataclasses.dataclass
-class LlamaConfig:
-    hidden: int = 2048
-    mlp: int = 8192
-    layers: int = 16
-    heads: int = 32
-    kv_heads: int = 8
-    head_dim: int = 64
-    vocab: int = 128256
-    rms_eps: float = 1e-5
-    rope_theta: float = 500000.0
+# Model shape and weights: stride_amd.weights (checkpoint loading or random init).
+LlamaConfig = ModelConfig
 
 
-def rope_table(cfg: LlamaConfig, positions: int) -> np.ndarray:
-    """[pos][head_dim/2][cos, sin] fp32, frequency theta^(-2i/D) (no llama3 scaling)."""
-    half = cfg.head_dim // 2
-    inv = cfg.rope_theta ** (-np.arange(half, dtype=np.float64) * 2.0 / cfg.head_dim)
-    ang = np.arange(positions, dtype=np.float64)[:, None] * inv[None, :]
-    return np.stack([np.cos(ang), np.sin(ang)], axis=-1).astype(np.float32)
-
-
-class Weights:
-    """Random-init weights in the tile formats the operators consume."""
-
-    def __init__(self, cfg: LlamaConfig, device, seed: int = 0, max_positions: int = 4096):
-        self.cfg = cfg
-        g = torch.Generator(device=device).manual_seed(seed)
-        D, H = cfg.head_dim, cfg.hidden
-
-        def w(n, k, rows=None):
-            t = (torch.randn(n, k, generator=g, device=device) * 0.02).to(torch.bfloat16).view(torch.int16)
-            return layout.pack_tiles(t, rows)
-
-        self.embed = w(cfg.vocab, H)  # tied with the LM head
-        self.layers = []
-        for _ in range(cfg.layers):
-            self.layers.append(dict(
-                q=w(cfg.heads * D, H, layout.rope_rows(cfg.heads * D, D)),
-                k=w(cfg.kv_heads * D, H, layout.rope_rows(cfg.kv_heads * D, D)),
-                v=w(cfg.kv_heads * D, H, layout.rope_rows(cfg.kv_heads * D, D)),
-                o=w(H, cfg.heads * D), w1=w(cfg.mlp, H), w3=w(cfg.mlp, H), w2=w(H, cfg.mlp),
-                norm_attn=torch.ones(H, device=device), norm_mlp=torch.ones(H, device=device)))
-        self.norm_final = torch.ones(H, device=device)
-        self.rope = torch.from_numpy(rope_table(cfg, max_positions)).to(device)
+def Weights(cfg: ModelConfig, device, seed: int = 0, max_positions: int = 4097) -> PackedWeights:
+    """Random-init weights of shape `cfg` (no checkpoint); see
+    stride_amd.weights.Weights.load for real checkpoints."""
+    return PackedWeights.random(cfg, device, seed, max_positions)
 
 
 @dataclasses.dataclass
@@ -107,6 +74,8 @@ class Engine:
         self.w = weights
         cfg = self.cfg = weights.cfg
         dev = self.dev = weights.embed.device
+        if cfg.head_dim not in (32, 64, 128) or cfg.repeat() != 4:
+            raise ValueError("the tensor-core attention serves head_dim 32/64/128 with four query heads per KV head")
         self.max_rows = max_rows
         self.max_pages = (max_ctx + 63) // 64
         lt = (max_rows + 15) // 16
@@ -150,7 +119,7 @@ class Engine:
             harness.compact(self.x, greedy, out_tiles=self.lm_x)
             x = self.lm_x
         best.copy_(self.best_init[:count])
-        harness.lm_greedy(w.embed, x, count, cfg.vocab, best=best)
+        harness.lm_greedy(w.lm, x, count, cfg.vocab, best=best)
 
     def device_rows(self, rows):
         """Device tensors (slot, pos, tok, items) for rows [(slot, pos, token)];
@@ -211,10 +180,10 @@ class Engine:
                 self._record(s, idx, val)
 
 
-def run(batch: int, prompt_len: int, new_tokens: int, device="cuda:0", seed: int = 0, cfg: LlamaConfig | None = None,
+def run(batch: int, prompt_len: int, new_tokens: int, device="cuda:0", seed: int = 0, cfg: ModelConfig | None = None,
         page_tokens: int = 16, max_rows: int = 4096, shuffle_seed: int = 0, perm_seed: int = 0, weights=None):
     """Greedy decode of `batch` random prompts; returns the sequences."""
-    cfg = cfg or LlamaConfig()
+    cfg = cfg or ModelConfig()
     weights = weights or Weights(cfg, device, seed)
     rng = np.random.default_rng(seed + 1)
     prompts = [rng.integers(0, cfg.vocab, prompt_len).tolist() for _ in range(batch)]

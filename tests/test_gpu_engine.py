@@ -44,3 +44,40 @@ def test_config5_batch_equals_alone():
         assert s.fingerprint == seqs[i].fingerprint
     assert len(set(tuple(s.tokens) for s in seqs)) > 1
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("tied", [True, False])
+def test_loaded_checkpoint_matches_float64_forward(tmp_path, tied):
+    """A tiny Llama checkpoint (llama3 RoPE, GQA 4:1, non-unit norm gains) loaded
+    by stride_amd.weights and decoded by the engine: every greedy token's logit
+    (fp32 bits returned by the LM head) must equal a float64 forward of the same
+    model that rounds to bf16 where the path stores bf16, within 0.02 (logits
+    have std ~1 here), and the token must be the float64 argmax unless the top
+    two are within that margin. Then batch vs alone must agree bit for bit."""
+    from stride_amd import weights
+    import llama_tiny
+
+    t, c = llama_tiny.write(str(tmp_path), seed=11, tied=tied)
+    say("loaded checkpoint: tied", tied)
+    w = weights.Weights.load(str(tmp_path), DEV, max_positions=64)
+    rope = w.rope.cpu().numpy()
+    rng = np.random.default_rng(12)
+    prompts = [rng.integers(0, c["vocab_size"], n).tolist() for n in (5, 19, 33)]
+    eng = engine.Engine(w, slots=3, max_ctx=48, max_rows=64, page_tokens=16, shuffle_seed=2)
+    seqs = [engine.Sequence(i, p) for i, p in enumerate(prompts)]
+    eng.prefill(seqs)
+    eng.decode(seqs, 3, perm_seed=3)
+    tol = 0.02
+    for s in seqs:
+        toks = list(s.prompt)
+        for tok, vbits in zip(s.tokens, s.values):
+            ref = llama_tiny.forward_last_logits(t, c, toks, rope)
+            val = float(np.uint32(vbits).view(np.float32))
+            assert abs(val - ref[tok]) <= tol, (val, ref[tok])
+            assert ref[tok] >= ref.max() - 2 * tol
+            toks.append(tok)
+    solo = engine.Engine(w, slots=1, max_ctx=48, max_rows=64, page_tokens=16)
+    s1 = engine.Sequence(0, prompts[2])
+    solo.prefill([s1])
+    solo.decode([s1], 3)
+    assert s1.tokens == seqs[2].tokens and s1.values == seqs[2].values and s1.fingerprint == seqs[2].fingerprint
