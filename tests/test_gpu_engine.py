@@ -51,9 +51,9 @@ def test_loaded_checkpoint_matches_float64_forward(tmp_path, tied):
     """A tiny Llama checkpoint (llama3 RoPE, GQA 4:1, non-unit norm gains) loaded
     by stride_amd.weights and decoded by the engine: every greedy token's logit
     (fp32 bits returned by the LM head) must equal a float64 forward of the same
-    model that rounds to bf16 where the path stores bf16, within 0.02 (logits
-    have std ~1 here), and the token must be the float64 argmax unless the top
-    two are within that margin. Then batch vs alone must agree bit for bit."""
+    model that rounds to bf16 where the path stores bf16, within 2e-3 of the
+    largest logit magnitude, and the token must be the float64 argmax unless the
+    top two are within that margin. Then batch vs alone must agree bit for bit."""
     from stride_amd import weights
     import llama_tiny
 
@@ -67,11 +67,11 @@ def test_loaded_checkpoint_matches_float64_forward(tmp_path, tied):
     seqs = [engine.Sequence(i, p) for i, p in enumerate(prompts)]
     eng.prefill(seqs)
     eng.decode(seqs, 3, perm_seed=3)
-    tol = 0.02
     for s in seqs:
         toks = list(s.prompt)
         for tok, vbits in zip(s.tokens, s.values):
             ref = llama_tiny.forward_last_logits(t, c, toks, rope)
+            tol = 2e-3 * np.abs(ref).max()
             val = float(np.uint32(vbits).view(np.float32))
             assert abs(val - ref[tok]) <= tol, (val, ref[tok])
             assert ref[tok] >= ref.max() - 2 * tol
