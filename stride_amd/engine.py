@@ -36,11 +36,18 @@ FNV_PRIME = 1099511628211
 MASK64 = (1 << 64) - 1
 
 
-def fnv_mix(h: int, v: int) -> int:
-    for i in range(4):
-        h ^= (v >> (8 * i)) & 0xFF
+def fnv_bytes(h: int, data: bytes) -> int:
+    """64-bit FNV-1a over `data`, continuing from state h."""
+    for byte in data:
+        h ^= byte
         h = (h * FNV_PRIME) & MASK64
     return h
+
+
+def fnv_mix(h: int, v: int) -> int:
+    """FNV-1a over the four little-endian bytes of a 32-bit value
+    (src/scheduler.cpp:15-24)."""
+    return fnv_bytes(h, (v & 0xFFFFFFFF).to_bytes(4, "little"))
 
 
 # Model shape and weights: stride_amd.weights (checkpoint loading or random init).

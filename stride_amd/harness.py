@@ -92,6 +92,15 @@ class PagedKv:
         ref = KvRef(ptr(arena), ptr(table), block, layer, which, group, max_blocks, head_dim)
         return PagedKv(arena, table, ref, page_tokens, max_blocks)
 
+    @property
+    def slots(self) -> int:
+        return int(self.table.shape[0])
+
+    @property
+    def capacity(self) -> int:
+        """Positions per slot."""
+        return self.max_blocks * self.page_tokens
+
     def gather(self, layer: int, which: int, slots, positions, kv_heads: int, head_dim: int) -> torch.Tensor:
         """Dense [rows][kv_heads * head_dim] bf16 bits of the entries at (slot, pos)."""
         r = self.ref

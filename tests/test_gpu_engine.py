@@ -81,3 +81,32 @@ def test_loaded_checkpoint_matches_float64_forward(tmp_path, tied):
     solo.prefill([s1])
     solo.decode([s1], 3)
     assert s1.tokens == seqs[2].tokens and s1.values == seqs[2].values and s1.fingerprint == seqs[2].fingerprint
+
+
+def test_ledger_identical_across_scheduling(tmp_path):
+    """stride_amd.cli on a tiny checkpoint: the JSONL ledger (tokens, logit bits,
+    fingerprints) must be byte-identical whether sequences run one at a time or
+    three at a time with a 16-row budget (prompts split across steps), shuffled
+    rows and shuffled KV pages."""
+    import json
+    from stride_amd import cli
+    import llama_tiny
+
+    llama_tiny.write(str(tmp_path / "m"), seed=5)
+    rng = np.random.default_rng(6)
+    with open(tmp_path / "p.jsonl", "w") as f:
+        for i, n in enumerate((3, 17, 9, 30, 1)):
+            f.write(json.dumps({"id": 10 + i, "tokens": rng.integers(0, 1000, n).tolist()}) + "\n")
+    say("ledger: sequential")
+    assert cli.main(["--model", str(tmp_path / "m"), "--input", str(tmp_path / "p.jsonl"), "--output",
+                     str(tmp_path / "a.jsonl"), "--max-new", "6"]) == 0
+    say("ledger: batched")
+    assert cli.main(["--model", str(tmp_path / "m"), "--input", str(tmp_path / "p.jsonl"), "--output",
+                     str(tmp_path / "b.jsonl"), "--max-new", "6", "--concurrency", "3", "--max-rows", "16",
+                     "--row-shuffle", "5", "--kv-shuffle", "7"]) == 0
+    a, b = (tmp_path / "a.jsonl").read_text(), (tmp_path / "b.jsonl").read_text()
+    assert a == b
+    recs = [json.loads(line) for line in a.splitlines()]
+    assert [r["id"] for r in recs] == [10, 11, 12, 13, 14] and all(len(r["tokens"]) == 6 for r in recs)
+    assert all(cli.hex64(cli.fingerprint(r["tokens"], [int(v, 16) for v in r["values"]])) == r["fingerprint"]
+               for r in recs)
