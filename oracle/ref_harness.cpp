@@ -5,7 +5,7 @@
 //
 // The harness converts plain row-major operands into the exact path's layouts:
 //   weights  W[group][col][4 rows]           (pack, src/model.cpp:94-111)
-//   RoPE rows (d0, d0+1, d0+D/2, d0+D/2+1)   (rope_rows, src/model.cpp:170-176)
+//   RoPE rows (d0, d0+1, d0+D/2, d0+D/2+1)   (rope_rows, src/model.cpp:168-174)
 //   activations dim-major A[dim*stride+lane] (src/kernels.h:3-8, lane_shape
 //                                             src/engine.cpp:24-28)
 // and calls k_lm_full / k_gemm_residual / k_mlp13 / k_lm_greedy / k_qkv, and

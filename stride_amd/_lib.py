@@ -16,11 +16,11 @@ LIB_PATH = os.path.join(HERE, "libstride_tc.so")
 EINVAL = 0x5354
 
 
-class GemmMat(C.Structure):  # src/kernels.h:112-116
+class GemmMat(C.Structure):  # src/kernels.h:23-27
     _fields_ = [("w", C.c_void_p), ("groups", C.c_int32), ("cols", C.c_int32)]
 
 
-class KvRef(C.Structure):  # src/kernels.h:119-128
+class KvRef(C.Structure):  # src/kernels.h:30-39
     _fields_ = [
         ("arena", C.c_void_p),
         ("table", C.c_void_p),
@@ -33,11 +33,11 @@ class KvRef(C.Structure):  # src/kernels.h:119-128
     ]
 
 
-class Lanes(C.Structure):  # src/kernels.h:130-135
+class Lanes(C.Structure):  # src/kernels.h:41-46
     _fields_ = [("rows", C.c_int32), ("lane_groups", C.c_int32), ("stride", C.c_int32), ("bug", C.c_int32)]
 
 
-class BestEntry(C.Structure):  # src/kernels.h:214-217
+class BestEntry(C.Structure):  # src/kernels.h:125-128
     _fields_ = [("value", C.c_float), ("index", C.c_int32)]
 
 
@@ -116,7 +116,58 @@ class AttentionParams(C.Structure):  # src/kernels.h:79-98
     ]
 
 
-# Symbols the library must export (everything include/stride_tc.h declares).
+# Exact-path parameter blocks (include/stride_exact.h, src/kernels.h:48-143).
+class EmbedParams(C.Structure):
+    _fields_ = [("l", Lanes), ("embed", C.c_void_p), ("tokens", C.c_void_p), ("h", C.c_void_p), ("dim", C.c_int32)]
+
+
+class NormParams(C.Structure):
+    _fields_ = [("l", Lanes), ("in_", C.c_void_p), ("out", C.c_void_p), ("weight", C.c_void_p), ("dim", C.c_int32),
+                ("eps", C.c_float)]
+
+
+class QkvParams(C.Structure):
+    _fields_ = [("l", Lanes), ("x", C.c_void_p), ("q", GemmMat), ("k", GemmMat), ("v", GemmMat), ("q_out", C.c_void_p),
+                ("q_stride", C.c_int32), ("kv", KvRef), ("rope", C.c_void_p), ("row_slot", C.c_void_p),
+                ("row_pos", C.c_void_p), ("layer", C.c_int32), ("head_dim", C.c_int32)]
+
+
+class GemmResidualParams(C.Structure):
+    _fields_ = [("l", Lanes), ("x", C.c_void_p), ("m", GemmMat), ("h", C.c_void_p)]
+
+
+class Mlp13Params(C.Structure):
+    _fields_ = [("l", Lanes), ("x", C.c_void_p), ("w1", GemmMat), ("w3", GemmMat), ("z", C.c_void_p)]
+
+
+class CompactParams(C.Structure):
+    _fields_ = [("l", Lanes), ("in_", C.c_void_p), ("out", C.c_void_p), ("lm_rows", C.c_void_p),
+                ("lm_count", C.c_int32), ("lm_stride", C.c_int32), ("dim", C.c_int32)]
+
+
+class LmGreedyParams(C.Structure):
+    _fields_ = [("l", Lanes), ("x", C.c_void_p), ("m", GemmMat), ("vocab", C.c_int32), ("best", C.c_void_p)]
+
+
+class LmFullParams(C.Structure):
+    _fields_ = [("l", Lanes), ("x", C.c_void_p), ("m", GemmMat), ("logits", C.c_void_p)]
+
+
+EXACT_ENTRIES = {  # name -> (params type, takes J)
+    "stride_k_embed": (EmbedParams, False),
+    "stride_k_norm": (NormParams, True),
+    "stride_k_qkv": (QkvParams, True),
+    "stride_k_attention": (AttentionParams, False),
+    "stride_k_gemm_residual": (GemmResidualParams, True),
+    "stride_k_mlp13": (Mlp13Params, True),
+    "stride_k_compact": (CompactParams, False),
+    "stride_k_lm_greedy": (LmGreedyParams, True),
+    "stride_k_lm_full": (LmFullParams, True),
+}
+
+
+# Symbols the library must export (everything include/stride_tc.h and
+# include/stride_exact.h declare).
 EXPORTS = (
     "stride_tc_qkv",
     "stride_tc_gemm_residual",
@@ -137,7 +188,7 @@ EXPORTS = (
     "stride_tc_dec_config_count",
     "stride_tc_stream_config",
     "stride_tc_last_stream_config",
-)
+) + tuple(EXACT_ENTRIES)
 
 
 def check_layout() -> None:
@@ -154,6 +205,10 @@ def check_layout() -> None:
     assert C.sizeof(TcGemmF32xParams) == 56
     assert C.sizeof(TcEmbedParams) == 48 and C.sizeof(TcNormParams) == 48 and C.sizeof(TcCompactParams) == 48
     assert AttentionParams.kv.offset == 48 and C.sizeof(AttentionParams) == 176
+    assert C.sizeof(EmbedParams) == 48 and C.sizeof(NormParams) == 48
+    assert QkvParams.kv.offset == 88 and QkvParams.rope.offset == 144 and C.sizeof(QkvParams) == 176
+    assert C.sizeof(GemmResidualParams) == 48 and C.sizeof(Mlp13Params) == 64 and C.sizeof(CompactParams) == 56
+    assert LmGreedyParams.best.offset == 48 and C.sizeof(LmGreedyParams) == 56 and C.sizeof(LmFullParams) == 48
 
 
 class StrideTcError(RuntimeError):
@@ -191,6 +246,10 @@ def load(path: str = LIB_PATH) -> C.CDLL:
                  "stride_tc_split_count"):
         getattr(lib, name).restype = C.c_int
     lib.stride_tc_split_count.argtypes = [C.c_int32, C.c_int32]
+    for name, (ptype, with_j) in EXACT_ENTRIES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = [C.POINTER(ptype), C.c_int32, vp] if with_j else [C.POINTER(ptype), vp]
+        fn.restype = C.c_int
     lib.stride_tc_set_stream_config.argtypes = [C.c_int32]
     lib.stride_tc_set_stream_config.restype = C.c_int
     lib.stride_tc_stream_config_count.argtypes = []

@@ -19,7 +19,7 @@ from concurrent.futures import ThreadPoolExecutor
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_obj")
-SOURCES = [os.path.join(CSRC, "tc_gemm.hip"), os.path.join(CSRC, "tc_aux.hip")]
+SOURCES = [os.path.join(CSRC, "tc_gemm.hip"), os.path.join(CSRC, "tc_aux.hip"), os.path.join(CSRC, "exact.hip")]
 OUT = os.path.join(HERE, "libstride_tc.so")
 PROBE_SOURCES = [os.path.join(CSRC, "probe.hip")]
 PROBE_OUT = os.path.join(HERE, "libstride_probe.so")

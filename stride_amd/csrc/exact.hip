@@ -1,0 +1,472 @@
+// The exact path on gfx950: the reference's fused FP32 kernels (src/kernels.cu)
+// evaluated on the GPU with the same IEEE operations, in the same order, per
+// output element as the reference's CPU exact path, so the two agree bit for bit.
+//
+// Mapping. The reference runs one 32-thread block per (four-row weight group,
+// lane group). Here a 64-lane wavefront runs two such blocks side by side (lanes
+// 0-31 and 32-63); within a half, lane t is the reference's thread t and owns
+// the same 64-byte weight lines (l == t mod 32), chaining fmaf over their columns
+// in ascending order. The 32 partial sums go through LDS and are added left to
+// right by one lane per output, ((P0 + P1) + P2) + ... + P31. Built with
+// -ffp-contract=off, so only the explicit fmaf calls fuse; division and square
+// root are the correctly rounded ones. Nothing here depends on the batch: a
+// block's result depends on its own weight group and lane group only.
+#include <hip/hip_runtime.h>
+
+#include <string>
+
+#include "../../include/stride_exact.h"
+#include "tc_common.hpp"
+
+namespace stride_tc {
+
+int fail(int code, const std::string& msg);  // tc_gemm.hip
+
+namespace {
+
+constexpr int kChains = 32;  // partial chains per dot product (src/kernels.h kBlockThreads)
+
+__device__ __forceinline__ float lo_half(uint32_t v) { return f32_of(v << 16); }
+__device__ __forceinline__ float hi_half(uint32_t v) { return f32_of(v & 0xFFFF0000u); }
+
+// Chain t of the dot products of one four-row weight group (wg: [col][4] bf16)
+// with J lanes of x (dim-major, lane j of column c at x[c * stride + j]):
+// acc[r * J + j] for row r, lane j. Lines of 8 columns: t, t + 32, ...; each
+// line is four 16-byte words, word q holding columns k + 2q (rows 0-3 in its
+// first two 32-bit halves' bf16 pairs) and k + 2q + 1 (last two)
+// (src/kernels.cu:22-94).
+template <int J>
+__device__ __forceinline__ void chain(const uint16_t* wg, const float* x, int stride, int cols, int t,
+                                      float (&acc)[4 * J]) {
+#pragma unroll
+  for (int e = 0; e < 4 * J; ++e) acc[e] = 0.0f;
+  const int lines = cols / 8;
+  for (int line = t; line < lines; line += kChains) {
+    const int k = line * 8;
+    const u32x4* wl = reinterpret_cast<const u32x4*>(wg + static_cast<int64_t>(k) * 4);
+    const u32x4 v[4] = {wl[0], wl[1], wl[2], wl[3]};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int c = k + 2 * q + h;
+        const float w[4] = {lo_half(v[q][2 * h]), hi_half(v[q][2 * h]), lo_half(v[q][2 * h + 1]),
+                            hi_half(v[q][2 * h + 1])};
+        if constexpr (J == 1) {
+          const float xc = x[c];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[r] = __builtin_fmaf(w[r], xc, acc[r]);
+        } else {
+          const f32x4 xc = *reinterpret_cast<const f32x4*>(x + static_cast<int64_t>(c) * stride);
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[r * 4 + j] = __builtin_fmaf(w[r], xc[j], acc[r * 4 + j]);
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// GEMM-shaped operators: Op supplies the weight group(s) of a block and the
+// epilogue on the folded sums y[m][r * J + j].
+
+struct ResidualOp {  // src/kernels.cu:294-325
+  using Params = StrideGemmResidualParams;
+  static constexpr int kMats = 1;
+  static int groups(const Params& p) { return p.m.groups; }
+  __device__ static const uint16_t* w(const Params& p, int, int group, int& cols) {
+    cols = p.m.cols;
+    return p.m.w + static_cast<int64_t>(group) * p.m.cols * 4;
+  }
+  template <int J>
+  __device__ static void finish(const Params& p, int group, int lg, int t, const float (*y)[16]) {
+    if (t >= 4 * J) return;
+    const int r = t / J, jj = t % J;
+    float* h = p.h + static_cast<int64_t>(group * 4 + r) * p.l.stride + lg * 4 + jj;
+    h[0] = h[0] + y[0][t];
+  }
+};
+
+struct Mlp13Op {  // src/kernels.cu:329-363
+  using Params = StrideMlp13Params;
+  static constexpr int kMats = 2;
+  static int groups(const Params& p) { return p.w1.groups; }
+  __device__ static const uint16_t* w(const Params& p, int m, int group, int& cols) {
+    const StrideGemmMat& mm = m == 0 ? p.w1 : p.w3;
+    cols = mm.cols;
+    return mm.w + static_cast<int64_t>(group) * mm.cols * 4;
+  }
+  template <int J>
+  __device__ static void finish(const Params& p, int group, int lg, int t, const float (*y)[16]) {
+    if (t >= 4 * J) return;
+    const int r = t / J, jj = t % J;
+    p.z[static_cast<int64_t>(group * 4 + r) * p.l.stride + lg * 4 + jj] = det_silu(y[0][t]) * y[1][t];
+  }
+};
+
+struct LmFullOp {  // src/kernels.cu:427-452
+  using Params = StrideLmFullParams;
+  static constexpr int kMats = 1;
+  static int groups(const Params& p) { return p.m.groups; }
+  __device__ static const uint16_t* w(const Params& p, int, int group, int& cols) {
+    cols = p.m.cols;
+    return p.m.w + static_cast<int64_t>(group) * p.m.cols * 4;
+  }
+  template <int J>
+  __device__ static void finish(const Params& p, int group, int lg, int t, const float (*y)[16]) {
+    if (t >= 4 * J) return;
+    const int r = t / J, jj = t % J;
+    p.logits[static_cast<int64_t>(group * 4 + r) * p.l.stride + lg * 4 + jj] = y[0][t];
+  }
+};
+
+struct LmGreedyOp {  // src/kernels.cu:383-425
+  using Params = StrideLmGreedyParams;
+  static constexpr int kMats = 1;
+  static int groups(const Params& p) { return p.m.groups; }
+  __device__ static const uint16_t* w(const Params& p, int, int group, int& cols) {
+    cols = p.m.cols;
+    return p.m.w + static_cast<int64_t>(group) * p.m.cols * 4;
+  }
+  template <int J>
+  __device__ static void finish(const Params& p, int group, int lg, int t, const float (*y)[16]) {
+    if (t >= J) return;
+    const int lane = lg * 4 + t;
+    if (lane >= p.l.rows) return;
+    float best = f32_of(0xFF800000u);
+    int32_t best_i = -1;
+    for (int r = 0; r < 4; ++r) {
+      const int index = group * 4 + r;
+      if (index >= p.vocab) continue;
+      const float v = y[0][r * J + t];
+      if (v > best) {
+        best = v;
+        best_i = index;
+      }
+    }
+    if (best_i >= 0) best_update(&p.best[lane], best, best_i);
+  }
+};
+
+struct QkvOp {  // src/kernels.cu:204-284
+  using Params = StrideQkvParams;
+  static constexpr int kMats = 1;
+  static int groups(const Params& p) { return p.q.groups + 2 * p.k.groups; }
+  __device__ static const uint16_t* w(const Params& p, int, int gi, int& cols) {
+    const StrideGemmMat& m = gi < p.q.groups ? p.q : (gi < p.q.groups + p.k.groups ? p.k : p.v);
+    const int group = gi < p.q.groups ? gi : (gi < p.q.groups + p.k.groups ? gi - p.q.groups : gi - p.q.groups - p.k.groups);
+    cols = m.cols;
+    return m.w + static_cast<int64_t>(group) * m.cols * 4;
+  }
+  template <int J>
+  __device__ static void finish(const Params& p, int gi, int lg, int t, const float (*y)[16]) {
+    if (t >= J) return;
+    const int j = lg * 4 + t;
+    if (j >= p.l.rows) return;
+    const int kind = gi < p.q.groups ? 0 : (gi < p.q.groups + p.k.groups ? 1 : 2);
+    const int group = kind == 0 ? gi : (kind == 1 ? gi - p.q.groups : gi - p.q.groups - p.k.groups);
+    const int D = p.head_dim, half = D / 2;
+    const int head = group / (D / 4);
+    const int d0 = 2 * (group % (D / 4));
+    const int pos = p.row_pos[j], slot = p.row_slot[j];
+    float a0 = y[0][0 * J + t], a1 = y[0][1 * J + t], b0 = y[0][2 * J + t], b1 = y[0][3 * J + t];
+    if (kind != 2) {
+      const float* cs = p.rope + (static_cast<int64_t>(pos) * half + d0) * 2;
+      const float c0 = cs[0], s0 = cs[1], c1 = cs[2], s1 = cs[3];
+      const float ra0 = a0 * c0 - b0 * s0, rb0 = b0 * c0 + a0 * s0;
+      const float ra1 = a1 * c1 - b1 * s1, rb1 = b1 * c1 + a1 * s1;
+      a0 = ra0;
+      b0 = rb0;
+      a1 = ra1;
+      b1 = rb1;
+    }
+    float* dst;
+    if (kind == 0) {
+      dst = p.q_out + static_cast<int64_t>(j) * p.q_stride + static_cast<int64_t>(head) * D;
+    } else {
+      const StrideKvRef& kv = p.kv;
+      const int64_t tokens = kv.group_elems / kv.head_dim;  // a power of two (checked on the host)
+      const int64_t block = kv.table[static_cast<int64_t>(slot) * kv.max_blocks + pos / tokens];
+      dst = static_cast<float*>(kv.arena) + block * kv.block_elems + p.layer * kv.layer_elems +
+            (kind - 1) * kv.which_elems + head * kv.group_elems + (pos % tokens) * kv.head_dim;
+    }
+    dst[d0] = a0;
+    dst[d0 + 1] = a1;
+    dst[d0 + half] = b0;
+    dst[d0 + half + 1] = b1;
+  }
+};
+
+// Two reference blocks per 64-lane workgroup: block = 2 * blockIdx.x + half,
+// (weight group, lane group) = (block / lane_groups, block % lane_groups).
+template <class Op, int J>
+__global__ __launch_bounds__(64) void k_exact_gemm(typename Op::Params p, int nblocks) {
+  constexpr int M = Op::kMats;
+  __shared__ float part[2][kChains][M][4 * J];
+  __shared__ float ys[2][M][16];
+  const int half = threadIdx.x >> 5, t = threadIdx.x & 31;
+  const int block = blockIdx.x * 2 + half;
+  const bool live = block < nblocks;
+  const int lg = live ? block % p.l.lane_groups : 0;
+  const int group = live ? block / p.l.lane_groups : 0;
+  if (live) {
+    const float* x = J == 1 ? p.x : p.x + lg * 4;
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      int cols = 0;
+      const uint16_t* wg = Op::w(p, m, group, cols);
+      float acc[4 * J];
+      chain<J>(wg, x, p.l.stride, cols, t, acc);
+#pragma unroll
+      for (int e = 0; e < 4 * J; ++e) part[half][t][m][e] = acc[e];
+    }
+  }
+  __syncthreads();
+  if (live && t < 4 * J) {
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      float y = part[half][0][m][t];
+      for (int i = 1; i < kChains; ++i) y = y + part[half][i][m][t];
+      ys[half][m][t] = y;
+    }
+  }
+  __syncthreads();
+  if (live) Op::template finish<J>(p, group, lg, t, ys[half]);
+}
+
+// ---------------------------------------------------------------------------
+// Embedding, RMSNorm, compaction.
+
+// h[k * stride + row] = widen(embed[token][k]); embed in [token/4][dim][4]
+// groups (src/kernels.cu:98-117).
+__global__ __launch_bounds__(64) void k_exact_embed(StrideEmbedParams p) {
+  const int row = blockIdx.x;
+  const int token = p.tokens[row];
+  const uint16_t* src = p.embed + static_cast<int64_t>(token / 4) * p.dim * 4 + token % 4;
+  for (int k = threadIdx.x; k < p.dim; k += 64)
+    p.h[static_cast<int64_t>(k) * p.l.stride + row] = f32_of(static_cast<uint32_t>(src[static_cast<int64_t>(k) * 4]) << 16);
+}
+
+// RMSNorm over four-dim units (src/kernels.cu:119-200): chain t sums the squares
+// of units u == t (mod 32) by fmaf, the 32 partials are added left to right,
+// r = 1 / sqrtf(sum / dim + eps), out = w * (v * r). One reference block (lane
+// group) per wavefront half.
+template <int J>
+__global__ __launch_bounds__(64) void k_exact_norm(StrideNormParams p) {
+  __shared__ float part[2][kChains][J];
+  __shared__ float rs[2][J];
+  const int half = threadIdx.x >> 5, t = threadIdx.x & 31;
+  const int block = blockIdx.x * 2 + half;
+  const bool live = block < p.l.lane_groups;
+  const int units = p.dim / 4, stride = p.l.stride;
+  const float* in = J == 1 ? p.in : p.in + (live ? block : 0) * 4;
+  float* out = J == 1 ? p.out : p.out + (live ? block : 0) * 4;
+  if (live) {
+    float acc[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) acc[j] = 0.0f;
+    for (int u = t; u < units; u += kChains) {
+      const int k = u * 4;
+      if constexpr (J == 1) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(in + k);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[0] = __builtin_fmaf(v[e], v[e], acc[0]);
+      } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const f32x4 v = *reinterpret_cast<const f32x4*>(in + static_cast<int64_t>(k + c) * stride);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[j] = __builtin_fmaf(v[j], v[j], acc[j]);
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < J; ++j) part[half][t][j] = acc[j];
+  }
+  __syncthreads();
+  if (live && t < J) {
+    float sum = part[half][0][t];
+    for (int i = 1; i < kChains; ++i) sum = sum + part[half][i][t];
+    rs[half][t] = 1.0f / sqrtf(sum / static_cast<float>(p.dim) + p.eps);
+  }
+  __syncthreads();
+  if (!live) return;
+  for (int u = t; u < units; u += kChains) {
+    const int k = u * 4;
+    const f32x4 w4 = *reinterpret_cast<const f32x4*>(p.weight + k);
+    if constexpr (J == 1) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(in + k);
+      const float r = rs[half][0];
+      f32x4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = w4[e] * (v[e] * r);
+      *reinterpret_cast<f32x4*>(out + k) = o;
+    } else {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int64_t at = static_cast<int64_t>(k + c) * stride;
+        const f32x4 v = *reinterpret_cast<const f32x4*>(in + at);
+        f32x4 o;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] = w4[c] * (v[j] * rs[half][j]);
+        *reinterpret_cast<f32x4*>(out + at) = o;
+      }
+    }
+  }
+}
+
+// out[k * lm_stride + l] = in[k * stride + lm_rows[l]] (src/kernels.cu:365-380).
+__global__ __launch_bounds__(64) void k_exact_compact(StrideCompactParams p) {
+  const int k = blockIdx.x * 64 + threadIdx.x;
+  if (k >= p.dim) return;
+  for (int l = 0; l < p.lm_count; ++l)
+    p.out[static_cast<int64_t>(k) * p.lm_stride + l] = p.in[static_cast<int64_t>(k) * p.l.stride + p.lm_rows[l]];
+}
+
+// ---------------------------------------------------------------------------
+// Host side.
+
+std::string lanes_why(const StrideLanes& l, int J) {
+  if (J != 1 && J != 4) return "J must be 1 or 4";
+  if (l.rows < 0) return "rows must be >= 0";
+  if (J == 1 && (l.rows > 1 || l.lane_groups != 1 || l.stride != 1)) return "J = 1 serves one row with lane_groups 1 and stride 1";
+  if (J == 4 && (l.lane_groups != (l.rows + 3) / 4 || l.stride < 4 * l.lane_groups || l.stride % 4 != 0))
+    return "J = 4 needs lane_groups = ceil(rows / 4) and a stride that is a multiple of 4 covering them";
+  return "";
+}
+
+std::string mat_why(const StrideGemmMat& m, const char* name) {
+  if (!m.w || m.groups <= 0 || m.cols <= 0 || m.cols % 8 != 0)
+    return std::string(name) + ": need a weight pointer, groups > 0 and cols a positive multiple of 8";
+  return "";
+}
+
+int launched(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(static_cast<int>(e), std::string(what) + " launch failed: " + hipGetErrorString(e));
+  return 0;
+}
+
+template <class Op>
+int run_gemm(const typename Op::Params& p, int J, void* stream, const char* what) {
+  const int nblocks = Op::groups(p) * p.l.lane_groups;
+  if (p.l.rows == 0 || nblocks == 0) return 0;
+  const dim3 grid((nblocks + 1) / 2);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (J == 1) hipLaunchKernelGGL((k_exact_gemm<Op, 1>), grid, dim3(64), 0, st, p, nblocks);
+  else hipLaunchKernelGGL((k_exact_gemm<Op, 4>), grid, dim3(64), 0, st, p, nblocks);
+  return launched(what);
+}
+
+}  // namespace
+}  // namespace stride_tc
+
+using namespace stride_tc;
+
+static_assert(sizeof(StrideEmbedParams) == 48, "EmbedParams layout");
+static_assert(sizeof(StrideNormParams) == 48, "NormParams layout");
+static_assert(offsetof(StrideQkvParams, kv) == 88 && offsetof(StrideQkvParams, rope) == 144 &&
+                  sizeof(StrideQkvParams) == 176, "QkvParams layout");
+static_assert(sizeof(StrideGemmResidualParams) == 48, "GemmResidualParams layout");
+static_assert(sizeof(StrideMlp13Params) == 64, "Mlp13Params layout");
+static_assert(sizeof(StrideCompactParams) == 56, "CompactParams layout");
+static_assert(offsetof(StrideLmGreedyParams, best) == 48 && sizeof(StrideLmGreedyParams) == 56, "LmGreedyParams layout");
+static_assert(sizeof(StrideLmFullParams) == 48, "LmFullParams layout");
+
+extern "C" {
+
+int stride_k_embed(const StrideEmbedParams* p, void* stream) {
+  if (!p) return fail(STRIDE_TC_EINVAL, "k_embed: null parameters");
+  if (p->l.rows < 0 || p->dim <= 0 || (p->l.rows > 0 && (!p->embed || !p->tokens || !p->h)) ||
+      p->l.stride < p->l.rows)
+    return fail(STRIDE_TC_EINVAL, "k_embed: need rows >= 0, dim > 0, stride >= rows and pointers");
+  if (p->l.rows == 0) return 0;
+  hipLaunchKernelGGL(k_exact_embed, dim3(p->l.rows), dim3(64), 0, static_cast<hipStream_t>(stream), *p);
+  return launched("k_embed");
+}
+
+int stride_k_norm(const StrideNormParams* p, int32_t J, void* stream) {
+  if (!p) return fail(STRIDE_TC_EINVAL, "k_norm: null parameters");
+  std::string why = lanes_why(p->l, J);
+  if (why.empty() && (p->dim <= 0 || p->dim % 4 != 0)) why = "dim must be a positive multiple of 4";
+  if (why.empty() && p->l.rows > 0 && (!p->in || !p->out || !p->weight)) why = "missing pointer";
+  if (!why.empty()) return fail(STRIDE_TC_EINVAL, "k_norm: " + why);
+  if (p->l.rows == 0) return 0;
+  const dim3 grid((p->l.lane_groups + 1) / 2);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (J == 1) hipLaunchKernelGGL(k_exact_norm<1>, grid, dim3(64), 0, st, *p);
+  else hipLaunchKernelGGL(k_exact_norm<4>, grid, dim3(64), 0, st, *p);
+  return launched("k_norm");
+}
+
+int stride_k_qkv(const StrideQkvParams* p, int32_t J, void* stream) {
+  if (!p) return fail(STRIDE_TC_EINVAL, "k_qkv: null parameters");
+  std::string why = lanes_why(p->l, J);
+  const int D = p->head_dim;
+  if (why.empty()) why = mat_why(p->q, "q");
+  if (why.empty()) why = mat_why(p->k, "k");
+  if (why.empty()) why = mat_why(p->v, "v");
+  if (why.empty() && (D <= 0 || D % 4 != 0 || p->kv.head_dim != D)) why = "head_dim must be a positive multiple of 4 matching kv.head_dim";
+  if (why.empty() && (p->k.groups != p->v.groups || p->q.cols != p->k.cols || p->k.cols != p->v.cols))
+    why = "k and v must have the same groups and all three the same cols";
+  if (why.empty()) {
+    const int64_t tokens = D > 0 ? p->kv.group_elems / D : 0;
+    if (tokens <= 0 || (tokens & (tokens - 1)) != 0) why = "the KV block (group_elems / head_dim) must be a power of two";
+  }
+  if (why.empty() && p->l.rows > 0 && (!p->x || !p->q_out || !p->rope || !p->row_slot || !p->row_pos || !p->kv.arena || !p->kv.table))
+    why = "missing pointer";
+  if (!why.empty()) return fail(STRIDE_TC_EINVAL, "k_qkv: " + why);
+  return run_gemm<QkvOp>(*p, J, stream, "k_qkv");
+}
+
+int stride_k_gemm_residual(const StrideGemmResidualParams* p, int32_t J, void* stream) {
+  if (!p) return fail(STRIDE_TC_EINVAL, "k_gemm_residual: null parameters");
+  std::string why = lanes_why(p->l, J);
+  if (why.empty()) why = mat_why(p->m, "m");
+  if (why.empty() && p->l.rows > 0 && (!p->x || !p->h)) why = "missing pointer";
+  if (!why.empty()) return fail(STRIDE_TC_EINVAL, "k_gemm_residual: " + why);
+  return run_gemm<ResidualOp>(*p, J, stream, "k_gemm_residual");
+}
+
+int stride_k_mlp13(const StrideMlp13Params* p, int32_t J, void* stream) {
+  if (!p) return fail(STRIDE_TC_EINVAL, "k_mlp13: null parameters");
+  std::string why = lanes_why(p->l, J);
+  if (why.empty()) why = mat_why(p->w1, "w1");
+  if (why.empty()) why = mat_why(p->w3, "w3");
+  if (why.empty() && (p->w1.groups != p->w3.groups || p->w1.cols != p->w3.cols)) why = "w1 and w3 must have the same shape";
+  if (why.empty() && p->l.rows > 0 && (!p->x || !p->z)) why = "missing pointer";
+  if (!why.empty()) return fail(STRIDE_TC_EINVAL, "k_mlp13: " + why);
+  return run_gemm<Mlp13Op>(*p, J, stream, "k_mlp13");
+}
+
+int stride_k_compact(const StrideCompactParams* p, void* stream) {
+  if (!p || p->lm_count < 0 || p->dim <= 0 || (p->lm_count > 0 && (!p->in || !p->out || !p->lm_rows)) ||
+      p->lm_stride < p->lm_count)
+    return fail(STRIDE_TC_EINVAL, "k_compact: need lm_count >= 0, dim > 0, lm_stride >= lm_count and pointers");
+  if (p->lm_count == 0) return 0;
+  hipLaunchKernelGGL(k_exact_compact, dim3((p->dim + 63) / 64), dim3(64), 0, static_cast<hipStream_t>(stream), *p);
+  return launched("k_compact");
+}
+
+int stride_k_lm_greedy(const StrideLmGreedyParams* p, int32_t J, void* stream) {
+  if (!p) return fail(STRIDE_TC_EINVAL, "k_lm_greedy: null parameters");
+  std::string why = lanes_why(p->l, J);
+  if (why.empty()) why = mat_why(p->m, "m");
+  if (why.empty() && (p->vocab <= 0 || p->vocab > p->m.groups * 4)) why = "vocab must be in (0, 4 * groups]";
+  if (why.empty() && p->l.rows > 0 && (!p->x || !p->best)) why = "missing pointer";
+  if (!why.empty()) return fail(STRIDE_TC_EINVAL, "k_lm_greedy: " + why);
+  return run_gemm<LmGreedyOp>(*p, J, stream, "k_lm_greedy");
+}
+
+int stride_k_lm_full(const StrideLmFullParams* p, int32_t J, void* stream) {
+  if (!p) return fail(STRIDE_TC_EINVAL, "k_lm_full: null parameters");
+  std::string why = lanes_why(p->l, J);
+  if (why.empty()) why = mat_why(p->m, "m");
+  if (why.empty() && p->l.rows > 0 && (!p->x || !p->logits)) why = "missing pointer";
+  if (!why.empty()) return fail(STRIDE_TC_EINVAL, "k_lm_full: " + why);
+  return run_gemm<LmFullOp>(*p, J, stream, "k_lm_full");
+}
+
+}  // extern "C"

@@ -14,6 +14,7 @@
 #include <cstddef>
 #include <string>
 
+#include "../../include/stride_exact.h"
 #include "tc_common.hpp"
 
 namespace stride_tc {
@@ -179,11 +180,12 @@ __global__ __launch_bounds__(64) void k_compact(StrideTcCompactParams p) {
 
 // K or V row of position pos for KV group `group` (src/kernel_common.h:20-25),
 // with the storage page given by the arena geometry.
-__device__ __forceinline__ const uint16_t* kv_row(const StrideKvRef& kv, int page_shift, int layer, int which, int group,
-                                                  int slot, int pos) {
+template <class KvT>
+__device__ __forceinline__ const KvT* kv_row(const StrideKvRef& kv, int page_shift, int layer, int which, int group,
+                                             int slot, int pos) {
   const int64_t block = kv.table[static_cast<int64_t>(slot) * kv.max_blocks + (pos >> page_shift)];
   const int token = pos & ((1 << page_shift) - 1);
-  return static_cast<const uint16_t*>(kv.arena) + block * kv.block_elems + layer * kv.layer_elems +
+  return static_cast<const KvT*>(kv.arena) + block * kv.block_elems + layer * kv.layer_elems +
          which * kv.which_elems + group * kv.group_elems + static_cast<int64_t>(token) * kv.head_dim;
 }
 
@@ -195,11 +197,14 @@ __device__ __forceinline__ const uint16_t* kv_row(const StrideKvRef& kv, int pag
 // then mixes the values of its dims over the positions in order; in the same
 // pass it adds the weights left to right, which yields the denominators (the
 // add and the mix see the weights in the same order) without a serial phase.
-template <int D>
+// KvT is uint16_t (bf16 KV, the tensor-core path) or float (the exact path);
+// the arithmetic is the same, on the widened values.
+template <int D, class KvT>
 __global__ __launch_bounds__(64) void k_attn_page(StrideAttentionParams p, int page_shift) {
-  constexpr int kPieces = kAttnPage * D / 8;  // 16-byte pieces of one page of V
-  constexpr int kPer = kPieces / 64;          // per lane
-  constexpr int kKey = D / 8;                 // 16-byte pieces of one K row
+  constexpr int kEl = 16 / static_cast<int>(sizeof(KvT));  // elements per 16-byte piece
+  constexpr int kPieces = kAttnPage * D / kEl;  // 16-byte pieces of one page of V
+  constexpr int kPer = kPieces / 64;            // per lane
+  constexpr int kKey = D / kEl;                 // 16-byte pieces of one K row
   const int item = blockIdx.x / p.n_kv;
   const int g = blockIdx.x % p.n_kv;
   const int lane = threadIdx.x;
@@ -211,7 +216,7 @@ __global__ __launch_bounds__(64) void k_attn_page(StrideAttentionParams p, int p
   const int n = min(visible - p0, kAttnPage);
   __shared__ f32x4 q4[D];        // the four heads' query values, per dim
   __shared__ f32x4 w4[kAttnPage];  // the four heads' weights, per position
-  __shared__ uint16_t vs[kAttnPage][D];
+  __shared__ KvT vs[kAttnPage][D];
 
   // Positions past the row's last one are clamped to it (their values are never
   // used), so every load is unconditional and stays inside the row's own pages.
@@ -219,13 +224,13 @@ __global__ __launch_bounds__(64) void k_attn_page(StrideAttentionParams p, int p
   u32x4 vr[kPer], kr[kKey];
 #pragma unroll
   for (int k = 0; k < kPer; ++k) {
-    const int P = k * 64 + lane, i = P / (D / 8), c = P % (D / 8);
-    vr[k] = load16(kv_row(p.kv, page_shift, p.layer, 1, g, slot, min(p0 + i, last)) + c * 8);
+    const int P = k * 64 + lane, i = P / (D / kEl), c = P % (D / kEl);
+    vr[k] = load16(kv_row<KvT>(p.kv, page_shift, p.layer, 1, g, slot, min(p0 + i, last)) + c * kEl);
   }
   {
-    const uint16_t* key = kv_row(p.kv, page_shift, p.layer, 0, g, slot, min(p0 + lane, last));
+    const KvT* key = kv_row<KvT>(p.kv, page_shift, p.layer, 0, g, slot, min(p0 + lane, last));
 #pragma unroll
-    for (int c = 0; c < kKey; ++c) kr[c] = load16(key + 8 * c);
+    for (int c = 0; c < kKey; ++c) kr[c] = load16(key + kEl * c);
   }
   const float* qrow = p.q + static_cast<int64_t>(j) * p.q_stride + static_cast<int64_t>(g * kHeadsPerGroup) * D;
   for (int d = lane; d < D; d += 64)
@@ -233,7 +238,7 @@ __global__ __launch_bounds__(64) void k_attn_page(StrideAttentionParams p, int p
 #pragma unroll
   for (int k = 0; k < kPer; ++k) {
     const int P = k * 64 + lane;
-    *reinterpret_cast<u32x4*>(&vs[P / (D / 8)][(P % (D / 8)) * 8]) = vr[k];
+    *reinterpret_cast<u32x4*>(&vs[P / (D / kEl)][(P % (D / kEl)) * kEl]) = vr[k];
   }
   __syncthreads();
 
@@ -241,9 +246,11 @@ __global__ __launch_bounds__(64) void k_attn_page(StrideAttentionParams p, int p
 #pragma unroll
   for (int c = 0; c < kKey; ++c) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float k = f32_of(e & 1 ? kr[c][e >> 1] & 0xFFFF0000u : kr[c][e >> 1] << 16);
-      const f32x4 qd = q4[8 * c + e];
+    for (int e = 0; e < kEl; ++e) {
+      float k;
+      if constexpr (kEl == 8) k = f32_of(e & 1 ? kr[c][e >> 1] & 0xFFFF0000u : kr[c][e >> 1] << 16);
+      else k = f32_of(kr[c][e]);
+      const f32x4 qd = q4[kEl * c + e];
       a0 = __builtin_fmaf(qd[0], k, a0);
       a1 = __builtin_fmaf(qd[1], k, a1);
       a2 = __builtin_fmaf(qd[2], k, a2);
@@ -274,7 +281,9 @@ __global__ __launch_bounds__(64) void k_attn_page(StrideAttentionParams p, int p
     f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f}, den = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll 4
     for (int i = 0; i < n; ++i) {
-      const float v = f32_of(static_cast<uint32_t>(vs[i][d]) << 16);
+      float v;
+      if constexpr (kEl == 8) v = f32_of(static_cast<uint32_t>(vs[i][d]) << 16);
+      else v = vs[i][d];
       const f32x4 wi = w4[i];
 #pragma unroll
       for (int h = 0; h < kHeadsPerGroup; ++h) {
@@ -295,11 +304,13 @@ __global__ __launch_bounds__(64) void k_attn_page(StrideAttentionParams p, int p
 }
 
 // Ascending-page combine of one row's records for one KV group, written as bf16
-// x tiles (src/kernel_common.h:252-309, writer src/kernels_tc.cu:658-666). All
+// x tiles (src/kernel_common.h:252-309, writer src/kernels_tc.cu:658-666) or,
+// for the exact path, as fp32 dim-major out[idx * stride + row] (LaneWriter,
+// src/kernels.cu:287-291). All
 // of the row's records come into LDS in one coalesced pass; threads 0..3 derive
 // each head's page factors and denominator (pages in order); thread (h, d) then
 // folds the weighted values of head h, dim d over the pages in order.
-template <int D>
+template <int D, bool kExact>
 __global__ __launch_bounds__(256) void k_attn_combine(StrideAttentionParams p) {
   extern __shared__ float recs[];  // [pages][rec_floats], then f[4][pages]
   __shared__ float den[kHeadsPerGroup];
@@ -335,7 +346,8 @@ __global__ __launch_bounds__(256) void k_attn_combine(StrideAttentionParams p) {
     float acc = 0.0f;
     for (int c = 0; c < pages; ++c) acc = __builtin_fmaf(f[qh * pages + c], recs[c * rf + 8 + qh * D + d], acc);
     const int idx = (g * p.n_q + qh) * D + d;
-    out[lane0 + static_cast<int64_t>(idx >> 4) * kTileElems + (idx & 15)] = static_cast<uint16_t>(bf16_rne(acc / den[qh]));
+    if constexpr (kExact) static_cast<float*>(p.out)[static_cast<int64_t>(idx) * p.l.stride + j] = acc / den[qh];
+    else out[lane0 + static_cast<int64_t>(idx >> 4) * kTileElems + (idx & 15)] = static_cast<uint16_t>(bf16_rne(acc / den[qh]));
   }
 }
 
@@ -359,17 +371,17 @@ static int launched(const char* what);
 // (The kernel's own static LDS shares the 160 KiB, hence the margin.)
 constexpr size_t kCombineLdsMax = 159 * 1024;
 
-template <int D>
+template <int D, bool kExact>
 static int combine(dim3 grid, size_t lds, hipStream_t st, const StrideAttentionParams& p) {
   static size_t raised = 64 * 1024;
   if (lds > raised) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn_combine<D>),
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn_combine<D, kExact>),
                                              hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
     if (e != hipSuccess) return fail(static_cast<int>(e), std::string("tc_attention: raising the LDS limit failed: ") + hipGetErrorString(e));
     raised = lds;
   }
-  hipLaunchKernelGGL(k_attn_combine<D>, grid, dim3(256), lds, st, p);
-  return launched("tc_attention (combine)");
+  hipLaunchKernelGGL((k_attn_combine<D, kExact>), grid, dim3(256), lds, st, p);
+  return launched("attention (combine)");
 }
 
 static int launched(const char* what) {
@@ -414,40 +426,53 @@ int stride_tc_compact(const StrideTcCompactParams* p, void* stream) {
   return launched("tc_compact");
 }
 
-int stride_tc_attention(const StrideAttentionParams* p, void* stream) {
-  if (!p) return fail(STRIDE_TC_EINVAL, "tc_attention: null parameters");
+}  // extern "C"
+
+// Shared checks and launches of the tensor-core (bf16 KV, bf16 x-tile output)
+// and exact (fp32 KV, fp32 dim-major output) attention.
+template <bool kExact>
+static int attention(const StrideAttentionParams* p, void* stream, const char* name) {
+  if (!p) return fail(STRIDE_TC_EINVAL, std::string(name) + ": null parameters");
   const int D = p->head_dim;
   const int64_t page_tokens = D > 0 ? p->kv.group_elems / D : 0;
   int page_shift = 0;
   while (page_shift < 30 && (int64_t{1} << page_shift) < page_tokens) ++page_shift;
   std::string why;
-  if (!lanes_valid(p->l)) why = "lane_groups must equal ceil(rows/16)";
+  if (kExact ? (p->l.rows < 0 || p->l.stride < p->l.rows) : !lanes_valid(p->l))
+    why = kExact ? "need rows >= 0 and stride >= rows" : "lane_groups must equal ceil(rows/16)";
   else if ((D != 32 && D != 64 && D != 128) || p->kv.head_dim != D) why = "head_dim must be 32, 64 or 128 and match kv.head_dim";
   else if (p->n_q != kHeadsPerGroup) why = "four query heads per KV group are required (the reference packs them in a float4)";
   else if (p->n_kv <= 0 || p->rec_floats < 8 + 4 * D || p->max_pages <= 0 || p->item_count < 0) why = "bad n_kv, rec_floats, max_pages or item_count";
   else if (page_tokens <= 0 || (int64_t{1} << page_shift) != page_tokens) why = "the KV storage page (group_elems / head_dim) must be a power of two";
-  else if (p->out_cols % 16 != 0 || p->out_cols < p->n_kv * p->n_q * D) why = "out_cols must be a multiple of 16 covering every head";
+  else if (!kExact && (p->out_cols % 16 != 0 || p->out_cols < p->n_kv * p->n_q * D)) why = "out_cols must be a multiple of 16 covering every head";
   else if (p->l.rows > 0 && (!p->q || !p->out || !p->kv.arena || !p->kv.table || !p->row_slot || !p->row_pos || !p->scratch ||
                              (p->item_count > 0 && !p->items)))
     why = "missing pointer";
   else if (static_cast<size_t>(p->max_pages) * (p->rec_floats + kHeadsPerGroup) * sizeof(float) > kCombineLdsMax)
     why = "max_pages * rec_floats too large for the combine's LDS (159 KiB)";
-  if (!why.empty()) return fail(STRIDE_TC_EINVAL, "tc_attention: " + why);
+  if (!why.empty()) return fail(STRIDE_TC_EINVAL, std::string(name) + ": " + why);
   if (p->l.rows == 0) return 0;
   hipStream_t st = static_cast<hipStream_t>(stream);
+  using KvT = typename std::conditional<kExact, float, uint16_t>::type;
   if (p->item_count > 0) {
     const dim3 grid(p->item_count * p->n_kv);
-    if (D == 32) hipLaunchKernelGGL(k_attn_page<32>, grid, dim3(64), 0, st, *p, page_shift);
-    else if (D == 64) hipLaunchKernelGGL(k_attn_page<64>, grid, dim3(64), 0, st, *p, page_shift);
-    else if (D == 128) hipLaunchKernelGGL(k_attn_page<128>, grid, dim3(64), 0, st, *p, page_shift);
-    else return fail(STRIDE_TC_EINVAL, "tc_attention: head_dim must be 32, 64 or 128");
-    if (int rc = launched("tc_attention (pages)")) return rc;
+    if (D == 32) hipLaunchKernelGGL((k_attn_page<32, KvT>), grid, dim3(64), 0, st, *p, page_shift);
+    else if (D == 64) hipLaunchKernelGGL((k_attn_page<64, KvT>), grid, dim3(64), 0, st, *p, page_shift);
+    else hipLaunchKernelGGL((k_attn_page<128, KvT>), grid, dim3(64), 0, st, *p, page_shift);
+    if (int rc = launched("attention (pages)")) return rc;
   }
   const size_t lds = static_cast<size_t>(p->max_pages) * (p->rec_floats + kHeadsPerGroup) * sizeof(float);
   const dim3 cgrid(p->l.rows * p->n_kv);
-  if (D == 32) return combine<32>(cgrid, lds, st, *p);
-  if (D == 64) return combine<64>(cgrid, lds, st, *p);
-  return combine<128>(cgrid, lds, st, *p);
+  if (D == 32) return combine<32, kExact>(cgrid, lds, st, *p);
+  if (D == 64) return combine<64, kExact>(cgrid, lds, st, *p);
+  return combine<128, kExact>(cgrid, lds, st, *p);
 }
 
-}  // extern "C"
+extern "C" int stride_tc_attention(const StrideAttentionParams* p, void* stream) {
+  return attention<false>(p, stream, "tc_attention");
+}
+
+// Exact path (src/kernels.cu:474-485): fp32 KV, fp32 dim-major output.
+extern "C" int stride_k_attention(const StrideAttentionParams* p, void* stream) {
+  return attention<true>(p, stream, "k_attention");
+}

@@ -1,6 +1,7 @@
 """C-ABI library checks that need no GPU: it loads, exports every symbol that
-include/stride_tc.h declares, its structs are byte-compatible with the reference's
-parameter blocks, the split rule, and argument rejection before any launch."""
+include/stride_tc.h and include/stride_exact.h declare, its structs are
+byte-compatible with the reference's parameter blocks, the split rule, and
+argument rejection before any launch."""
 import ctypes as C
 import os
 import re
@@ -13,12 +14,14 @@ from stride_amd import tc
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "stride_tc.h")
+EXACT_HEADER = os.path.join(ROOT, "include", "stride_exact.h")
 REF_SRC = "/root/reference/src"
 
 
 def test_exports_match_header():
     lib = _lib.load()
     declared = set(re.findall(r"\b(stride_tc_\w+)\s*\(", open(HEADER).read()))
+    declared |= set(re.findall(r"\b(stride_k_\w+)\s*\(", open(EXACT_HEADER).read()))
     assert declared == set(_lib.EXPORTS)
     for name in declared:
         assert hasattr(lib, name), name
@@ -67,6 +70,37 @@ def test_struct_layout_matches_reference(tmp_path):
                          LMG="stride::TcLmGreedyParams", EMB="stride::TcEmbedParams", NRM="stride::TcNormParams",
                          CMP="stride::TcCompactParams", ATT="stride::AttentionParams"))
     assert ours == theirs
+
+
+EXACT_PROBE = r"""
+#include <cstddef>
+#include <cstdio>
+#include HDR
+int main() {
+  printf("%zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu\n", sizeof(EMB), offsetof(EMB, dim), sizeof(NRM),
+         offsetof(NRM, eps), sizeof(QKV), offsetof(QKV, kv), offsetof(QKV, rope), offsetof(QKV, head_dim), sizeof(RES),
+         sizeof(MLP), offsetof(MLP, z), sizeof(CMP), offsetof(CMP, dim), sizeof(LMG), sizeof(LMF));
+}
+"""
+
+
+def test_exact_struct_layout_matches_reference(tmp_path):
+    names = dict(EMB="EmbedParams", NRM="NormParams", QKV="QkvParams", RES="GemmResidualParams", MLP="Mlp13Params",
+                 CMP="CompactParams", LMG="LmGreedyParams", LMF="LmFullParams")
+
+    def probe(include, prefix):
+        src = tmp_path / f"p{len(prefix)}.cpp"
+        defs = "".join(f"#define {k} {prefix}{v}\n" for k, v in names.items())
+        src.write_text(defs + EXACT_PROBE.replace("HDR", f'"{include}"'))
+        exe = tmp_path / f"p{len(prefix)}"
+        subprocess.run(["g++", "-std=c++17", str(src), "-o", str(exe)], check=True)
+        return subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split()
+
+    ours = probe(EXACT_HEADER, "Stride")
+    assert ours == ["48", "40", "48", "44", "176", "88", "144", "172", "48", "64", "56", "56", "48", "56", "48"]
+    if not os.path.exists(os.path.join(REF_SRC, "kernels.h")):
+        pytest.skip("reference tree absent")
+    assert probe(os.path.join(REF_SRC, "kernels.h"), "stride::") == ours
 
 
 def test_split_rule():
