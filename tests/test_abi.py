@@ -153,3 +153,24 @@ def test_cpp_shim_compiles_against_reference_header(tmp_path):
                  "stride::tc_lm_greedy(stride::TcLmGreedyParams const&, int, int)",
                  "stride::tc_lm_full(stride::TcLmFullParams const&, int)"):
         assert name in syms, name
+
+
+def test_exact_shim_compiles_against_reference_header(tmp_path):
+    """include/stride_exact_shim.hpp defines stride::k_* with the reference
+    signatures (src/kernels.h:146-155) over the C ABI, compiled against the
+    reference's own kernels.h together with the tensor-core shim."""
+    if not os.path.exists(os.path.join(REF_SRC, "kernels.h")):
+        pytest.skip("reference tree absent")
+    tu = tmp_path / "exact_hip.cpp"
+    tu.write_text('#include "kernels_tc.h"\n#include "stride_tc_shim.hpp"\n#include "stride_exact_shim.hpp"\n'
+                  'namespace stride { void* tc_stream() { return nullptr; } }\n')
+    subprocess.run(["g++", "-std=c++17", "-Wall", "-Werror", "-c", f"-I{REF_SRC}", f"-I{os.path.join(ROOT, 'include')}",
+                    str(tu), "-o", str(tmp_path / "tu.o")], check=True)
+    syms = subprocess.run(["nm", "-C", str(tmp_path / "tu.o")], capture_output=True, text=True, check=True).stdout
+    for name in ("stride::k_embed(stride::EmbedParams const&)", "stride::k_norm(stride::NormParams const&, int)",
+                 "stride::k_qkv(stride::QkvParams const&, int)", "stride::k_attention(stride::AttentionParams const&)",
+                 "stride::k_gemm_residual(stride::GemmResidualParams const&, int)",
+                 "stride::k_mlp13(stride::Mlp13Params const&, int)", "stride::k_compact(stride::CompactParams const&)",
+                 "stride::k_lm_greedy(stride::LmGreedyParams const&, int)",
+                 "stride::k_lm_full(stride::LmFullParams const&, int)"):
+        assert name in syms, name
