@@ -43,6 +43,12 @@ def parse():
     ap.add_argument("--table", type=int, default=1, help="per-GEMM table over M (0 to skip)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline budget (0 to skip)")
     ap.add_argument("--cpu-threads", type=int, default=16)
+    ap.add_argument("--library", type=int, default=1,
+                    help="also time torch.matmul (hipBLASLt) bf16 on the five shapes at M=4096 as context (0 to skip)")
+    ap.add_argument("--op", default="", help="time only this GEMM (qkv, o, gate_up, down, lm_head) at --m and print "
+                    "its JSON (for kernel-level profiles)")
+    ap.add_argument("--engine-only", type=int, default=0,
+                    help="run only the full decode step (for kernel profiles of it) and print its JSON")
     ap.add_argument("--engine", type=int, default=1,
                     help="also time one full decode step of the config-5 engine (0 to skip)")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
@@ -281,6 +287,32 @@ def engine_step(torch, dev, m, steps, warmup, position=383):
                    "tc_gemm_residual), tc_norm, tc_lm_greedy"}
 
 
+def library_gemm(torch, dev, m=4096):
+    """Context for the prefill roofline: the vendor library (torch.matmul, which
+    calls hipBLASLt) on the same shapes at M = m in bf16, weights rotated past the
+    MALL, HIP-graph timing. It has no batch-invariance contract and no fused
+    epilogue, so it is a ceiling reference, not a parity target."""
+    res = {}
+    shapes = {"qkv": (3072, HIDDEN), "o": (HIDDEN, HIDDEN), "gate_up": (2 * FFN, HIDDEN), "down": (HIDDEN, FFN),
+              "lm_head": (VOCAB, HIDDEN)}
+    for name, (n, k) in shapes.items():
+        a = torch.randn(m, k, device=dev, dtype=torch.bfloat16)
+        ws = [torch.randn(n, k, device=dev, dtype=torch.bfloat16) for _ in range(2 if n > 100000 else 8)]
+        g = capture(torch, [lambda w=w: torch.matmul(a, w.t()) for w in ws])
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        g.replay()
+        g.replay()
+        e1.record()
+        e1.synchronize()
+        sec = e0.elapsed_time(e1) / 1e3 / (2 * len(ws))
+        tfl = 2.0 * m * n * k / sec / 1e12
+        res[name] = {"us": round(sec * 1e6, 1), "TFLOP/s": round(tfl, 1), "frac": round(tfl / MFMA_BF16_PEAK_TFLOPS, 4)}
+        del g, ws, a
+        torch.cuda.empty_cache()
+    return res
+
+
 def main():
     a = parse()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -294,9 +326,22 @@ def main():
     _lib.load()  # fail loudly without the HIP library
     dev = "cuda:0"
     torch.cuda.set_device(0)
+    if a.engine_only:
+        print(json.dumps({"full_decode_step": engine_step(torch, dev, a.m, a.steps, a.warmup)}), flush=True)
+        return
     model = Model(torch, dev)
     b = Buffers(torch, dev, a.m)
     ops = step_ops(model, b)
+    if a.op:
+        sel = [(n, f) for n, f in ops if n == a.op]
+        if not sel:
+            print(f"bench.py: unknown --op {a.op}", file=sys.stderr)
+            sys.exit(2)
+        sec = time_ops(torch, sel, max(1, a.steps // len(sel)))[a.op]
+        f, byt = work(a.op, a.m)
+        print(json.dumps({"op": a.op, "M": a.m, "us": round(sec * 1e6, 2), "GB/s": round(byt / sec / 1e9, 1),
+                          "TFLOP/s": round(f / sec / 1e12, 1)}), flush=True)
+        return
 
     if a.copy_calib_mib:
         src = torch.ones(a.copy_calib_mib << 18, dtype=torch.float32, device=dev)
@@ -365,6 +410,7 @@ def main():
             torch.cuda.empty_cache()
 
     full = engine_step(torch, dev, a.m, a.steps, a.warmup) if a.engine else None
+    library = library_gemm(torch, dev) if a.library else None
     cpu = cpu_baseline(a.cpu_seconds, a.cpu_threads) if a.cpu_seconds > 0 else None
     out = {
         "metric": "Llama-3.2-1B GEMM GB/s & TFLOP/s (% roofline) at M=1..4096; decode tok/s",
@@ -376,6 +422,7 @@ def main():
                    "step_GB/s": round(weight_bytes / (ms_step / 1e3) / 1e9, 1), "parallelism": "single-gpu",
                    "launch": "HIP graph of one step, replayed", "eager_ms_per_step": round(eager_ms, 4)},
         "roofline": roof, "cpu_baseline": cpu, "full_decode_step": full, "gemm_table": table,
+        "library_gemm_m4096": library,
     }
     print(json.dumps(out), flush=True)
 

@@ -42,6 +42,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kTileElems = 256;     // one 16x16 tile
 constexpr int kChunkBytes = 1024;   // 32 columns of one row/lane tile (two tiles)
@@ -66,6 +67,49 @@ __device__ __forceinline__ u32x4 load16(const void* p) { return *reinterpret_cas
 
 __device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
+}
+
+// v_mfma_f32_32x32x16_bf16: A 32 rows x 16 k (lane l: row l%32, k 8*(l/32) ..
+// +7), B 16 k x 32 lanes (lane l: lane l%32, same k), C 32 x 32 (lane l: lane
+// l%32, rows 8*(i/4) + 4*(l/32) + i%4). Two of them over k 0-15 then 16-31 give
+// the same bits as one v_mfma_f32_16x16x32_bf16 per 16x16 tile over the 32-column
+// chunk (checked on the device by the shape-equivalence probe).
+__device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
+}
+
+// 16x16 tile (a, b) (row half a, lane half b) of a 32x32 accumulator, in the
+// 16x16x32 C layout (lane l: lane l%16, rows 4*(l/16) + j). Tile element (row
+// 4q + j, lane c) with q = l/16 sits in block lane (q%2)*32 + 16b + c, register
+// 4*(2a + q/2) + j. Every lane of the wavefront must call it.
+__device__ __forceinline__ f32x4 tile_of_block(const f32x16& v, int a, int b, int lane) {
+  const int q = lane >> 4;
+  const int src = ((q & 1) << 5) + (b << 4) + (lane & 15);
+  f32x4 out;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float v0 = __shfl(v[4 * (2 * a) + j], src);
+    const float v1 = __shfl(v[4 * (2 * a + 1) + j], src);
+    out[j] = (q >> 1) ? v1 : v0;
+  }
+  return out;
+}
+
+// Inverse: a 32x32 accumulator from its four 16x16 tiles t[a][b]. Block lane l,
+// register i holds row 8*(i/4) + 4*(l/32) + i%4, lane l%32: tile (i/8, (l%32)/16),
+// tile lane (2*((i/4)%2) + l/32)*16 + l%16, register i%4.
+__device__ __forceinline__ f32x16 block_of_tiles(const f32x4 (&t)[2][2], int lane) {
+  const int b = (lane >> 4) & 1;
+  f32x16 v;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int a = i >> 3;
+    const int src = ((2 * ((i >> 2) & 1) + (lane >> 5)) << 4) + (lane & 15);
+    const float x0 = __shfl(t[a][0][i & 3], src);
+    const float x1 = __shfl(t[a][1][i & 3], src);
+    v[i] = b ? x1 : x0;
+  }
+  return v;
 }
 
 __device__ __forceinline__ float f32_of(uint32_t u) { return __uint_as_float(u); }

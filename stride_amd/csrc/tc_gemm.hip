@@ -388,7 +388,7 @@ int launch_tile(Geometry g, const typename Epi::Out& o, hipStream_t st) {
   return 0;
 }
 
-template <class Epi, int WRT, int WLT, int WM, int WN, int KC, int NS, int OCC>
+template <class Epi, int WRT, int WLT, int WM, int WN, int KC, int NS, int OCC, int MF32 = 0>
 void launch_pipe(Geometry g, const typename Epi::Out& o, int smax, hipStream_t st) {
   constexpr int BR = WM * WRT, BL = WN * WLT;
   int blocks = 0;
@@ -397,52 +397,62 @@ void launch_pipe(Geometry g, const typename Epi::Out& o, int smax, hipStream_t s
     blocks += g.seg[i].blocks;
   }
   blocks *= (g.lane_groups + BL - 1) / BL;
-  if (smax > 1)
-    hipLaunchKernelGGL((k_pipe<Epi, WRT, WLT, WM, WN, KC, NS, OCC, true>), dim3(blocks), dim3(kWave * WM * WN), 0, st, g, o);
-  else
-    hipLaunchKernelGGL((k_pipe<Epi, WRT, WLT, WM, WN, KC, NS, OCC, false>), dim3(blocks), dim3(kWave * WM * WN), 0, st, g, o);
+  if constexpr (MF32) {
+    if (smax > 1)
+      hipLaunchKernelGGL((k_pipe32<Epi, WRT, WLT, WM, WN, KC, NS, OCC, true>), dim3(blocks), dim3(kWave * WM * WN), 0, st, g, o);
+    else
+      hipLaunchKernelGGL((k_pipe32<Epi, WRT, WLT, WM, WN, KC, NS, OCC, false>), dim3(blocks), dim3(kWave * WM * WN), 0, st, g, o);
+  } else {
+    if (smax > 1)
+      hipLaunchKernelGGL((k_pipe<Epi, WRT, WLT, WM, WN, KC, NS, OCC, true>), dim3(blocks), dim3(kWave * WM * WN), 0, st, g, o);
+    else
+      hipLaunchKernelGGL((k_pipe<Epi, WRT, WLT, WM, WN, KC, NS, OCC, false>), dim3(blocks), dim3(kWave * WM * WN), 0, st, g, o);
+  }
 }
 
-// Prefill configurations of k_pipe: (WRT, WLT, WM, WN, KC, NS, OCC). For the
-// paired gate/up GEMM WRT counts pairs and is halved (two matrices per row tile).
+// Prefill configurations of k_pipe: (WRT, WLT, WM, WN, KC, NS, OCC, MF32). For
+// the paired gate/up GEMM WRT counts pairs and is halved (two matrices per row
+// tile). MF32 = 1 runs k_pipe32 (32x32x16 MFMAs; same bits).
 // Index -3 - i in the tuning hook selects configuration i.
 #define STRIDE_TC_PIPE_CONFIGS(X) \
-  X(0, 4, 4, 2, 2, 2, 3, 1)       \
-  X(1, 4, 4, 4, 2, 2, 2, 1)       \
-  X(2, 4, 4, 2, 4, 2, 2, 1)       \
-  X(3, 8, 4, 2, 4, 2, 2, 1)       \
-  X(4, 4, 8, 4, 2, 2, 2, 1)       \
-  X(5, 4, 8, 2, 2, 2, 3, 1)       \
-  X(6, 4, 4, 4, 4, 2, 2, 1)       \
-  X(7, 8, 4, 2, 2, 2, 3, 1)       \
-  X(8, 4, 4, 4, 2, 2, 3, 1)       \
-  X(9, 4, 8, 2, 2, 2, 2, 1)       \
-  X(10, 4, 2, 1, 4, 2, 4, 1)      \
-  X(11, 4, 4, 1, 2, 2, 4, 1)      \
-  X(12, 2, 2, 2, 4, 2, 4, 1)      \
-  X(13, 2, 4, 1, 2, 2, 4, 1)      \
-  X(14, 4, 1, 1, 4, 2, 4, 1)      \
-  X(15, 2, 2, 1, 4, 2, 4, 2)      \
-  X(16, 4, 2, 2, 2, 2, 4, 1)      \
-  X(17, 4, 1, 1, 4, 2, 6, 1)       \
-  X(18, 4, 8, 4, 2, 1, 4, 1)      \
-  X(19, 4, 8, 4, 2, 1, 5, 1)      \
-  X(20, 8, 4, 2, 4, 1, 4, 1)      \
-  X(21, 4, 4, 4, 2, 1, 5, 1)      \
-  X(22, 4, 4, 4, 2, 1, 6, 1)      \
-  X(23, 4, 4, 2, 4, 1, 5, 1)      \
-  X(24, 8, 8, 2, 2, 1, 4, 1)      \
-  X(25, 4, 8, 2, 2, 1, 6, 1)
+  X(0, 4, 4, 2, 2, 2, 3, 1, 0) \
+  X(1, 4, 4, 4, 2, 2, 2, 1, 0) \
+  X(2, 4, 4, 2, 4, 2, 2, 1, 0) \
+  X(3, 8, 4, 2, 4, 2, 2, 1, 0) \
+  X(4, 4, 8, 4, 2, 2, 2, 1, 0) \
+  X(5, 4, 8, 2, 2, 2, 3, 1, 0) \
+  X(6, 4, 4, 4, 4, 2, 2, 1, 0) \
+  X(7, 8, 4, 2, 2, 2, 3, 1, 0) \
+  X(8, 4, 4, 4, 2, 2, 3, 1, 0) \
+  X(9, 4, 8, 2, 2, 2, 2, 1, 0) \
+  X(10, 4, 2, 1, 4, 2, 4, 1, 0) \
+  X(11, 4, 4, 1, 2, 2, 4, 1, 0) \
+  X(12, 2, 2, 2, 4, 2, 4, 1, 0) \
+  X(13, 2, 4, 1, 2, 2, 4, 1, 0) \
+  X(14, 4, 1, 1, 4, 2, 4, 1, 0) \
+  X(15, 2, 2, 1, 4, 2, 4, 2, 0) \
+  X(16, 4, 2, 2, 2, 2, 4, 1, 0) \
+  X(17, 4, 1, 1, 4, 2, 6, 1, 0) \
+  X(18, 4, 8, 4, 2, 1, 4, 1, 0) \
+  X(19, 4, 8, 4, 2, 1, 5, 1, 0) \
+  X(20, 8, 4, 2, 4, 1, 4, 1, 0) \
+  X(21, 4, 4, 4, 2, 1, 5, 1, 0) \
+  X(22, 4, 4, 4, 2, 1, 6, 1, 0) \
+  X(23, 4, 4, 2, 4, 1, 5, 1, 0) \
+  X(24, 8, 8, 2, 2, 1, 4, 1, 0) \
+  X(25, 4, 8, 2, 2, 1, 6, 1, 0) \
+  X(26, 4, 4, 4, 2, 2, 3, 1, 1) \
+  X(27, 4, 4, 2, 4, 1, 5, 1, 1)
 
-constexpr int kNumPipeCfgs = 26;
+constexpr int kNumPipeCfgs = 28;
 int g_forced_pipe = -1;
 
 template <class Epi>
 void launch_pipe_cfg(int idx, const Geometry& g, const typename Epi::Out& o, int smax, hipStream_t st) {
   switch (idx) {
-#define STRIDE_TC_PIPE_CASE(i, WRT, WLT, WM, WN, KC, NS, OCC)                                              \
-  case i:                                                                                                 \
-    launch_pipe<Epi, (Epi::kMats == 2 ? (WRT > 2 ? WRT / 2 : WRT) : WRT), WLT, WM, WN, KC, NS, OCC>(g, o, smax, st); \
+#define STRIDE_TC_PIPE_CASE(i, WRT, WLT, WM, WN, KC, NS, OCC, MF)                                                 \
+  case i:                                                                                                         \
+    launch_pipe<Epi, (Epi::kMats == 2 ? (WRT > 2 ? WRT / 2 : WRT) : WRT), WLT, WM, WN, KC, NS, OCC, MF>(g, o, smax, st); \
     break;
     STRIDE_TC_PIPE_CONFIGS(STRIDE_TC_PIPE_CASE)
 #undef STRIDE_TC_PIPE_CASE
@@ -465,7 +475,7 @@ int pick_pipe(const Geometry& g, int smax) {
 
 bool pipe_cfg_fits(int idx, const Geometry& g) {
   static const int kc[] = {
-#define STRIDE_TC_PIPE_KC(i, WRT, WLT, WM, WN, KC, NS, OCC) KC,
+#define STRIDE_TC_PIPE_KC(i, WRT, WLT, WM, WN, KC, NS, OCC, MF) KC,
       STRIDE_TC_PIPE_CONFIGS(STRIDE_TC_PIPE_KC)
 #undef STRIDE_TC_PIPE_KC
   };
@@ -483,12 +493,12 @@ constexpr int kStreamMaxLaneTiles = 8;
 // Row tiles per workgroup of prefill configuration idx.
 int pipe_rows_per_block(int idx, int mats) {
   static const int wrt[] = {
-#define STRIDE_TC_PIPE_WRT(i, WRT, WLT, WM, WN, KC, NS, OCC) WRT,
+#define STRIDE_TC_PIPE_WRT(i, WRT, WLT, WM, WN, KC, NS, OCC, MF) WRT,
       STRIDE_TC_PIPE_CONFIGS(STRIDE_TC_PIPE_WRT)
 #undef STRIDE_TC_PIPE_WRT
   };
   static const int wm[] = {
-#define STRIDE_TC_PIPE_WM(i, WRT, WLT, WM, WN, KC, NS, OCC) WM,
+#define STRIDE_TC_PIPE_WM(i, WRT, WLT, WM, WN, KC, NS, OCC, MF) WM,
       STRIDE_TC_PIPE_CONFIGS(STRIDE_TC_PIPE_WM)
 #undef STRIDE_TC_PIPE_WM
   };

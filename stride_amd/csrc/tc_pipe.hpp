@@ -257,4 +257,239 @@ __global__ __launch_bounds__(kWave * WM * WN, OCC) void k_pipe(Geometry g, typen
   });
 }
 
+
+// The same pipeline with v_mfma_f32_32x32x16_bf16: each wave owns WRT/2 x WLT/2
+// blocks of 32 rows x 32 lanes, and a 32-column chunk is two MFMAs per block
+// (columns 0-15, then 16-31), which gives the bits of the 16x16x32 form (see
+// mfma32) at half the instruction count - the form that keeps the matrix pipe
+// busy at one or two waves per SIMD. The LDS staging is unchanged: a lane reads
+// the 16 bytes of its 32x32x16 fragment (row or lane l%32 of the pair of tiles,
+// k half h, k group l/32) from the 16x16x32 fragment order of its tile's chunk.
+// Accumulators enter (h for the residual) and leave (the epilogues) as 16x16
+// tiles, converted with cross-lane shuffles.
+template <class Epi, int WRT, int WLT, int WM, int WN, int KC, int NS, int OCC, bool HASY>
+__global__ __launch_bounds__(kWave * WM * WN, OCC) void k_pipe32(Geometry g, typename Epi::Out o) {
+  static_assert(WRT % 2 == 0 && WLT % 2 == 0, "32x32 blocks need even tile counts per wave");
+  constexpr int M = Epi::kMats;
+  constexpr int NW = WM * WN;
+  constexpr int BR = WM * WRT, BL = WN * WLT;
+  constexpr int PR = WRT / 2, PL = WLT / 2;         // 32x32 blocks per wave (rows, lanes)
+  constexpr int NBLK = (M * BR + BL) * KC;          // 1 KiB chunks per stage
+  static_assert(NBLK % NW == 0, "stage copies must split evenly over the waves");
+  constexpr int PER_WAVE = NBLK / NW;
+  constexpr int STAGE = NBLK * kWave;
+  __shared__ u32x4 ring[NS * STAGE];
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int wr = wave / WN, wn = wave % WN;
+  const int lblocks = (g.lane_groups + BL - 1) / BL;
+
+  int b = xcd_remap(blockIdx.x, gridDim.x);
+  const int si = locate_segment(g, b, lblocks);
+  const Segment sg = seg_at(g, si);
+  constexpr int G = 8;
+  const int group = b / (G * lblocks);
+  const int gsize = min(G, sg.blocks - group * G);
+  const int within = b % (G * lblocks);
+  const int rb = group * G + within % gsize;
+  const int lb = within / gsize;
+  const int rt0 = rb * BR, lt0 = lb * BL;
+
+  const int chunks = g.col_tiles >> 1;
+  const int per = chunks / sg.splits;
+  const int nst = chunks / KC;
+  const int64_t strip = static_cast<int64_t>(g.col_tiles) * kTileElems;
+  const int foff = frag_offset(lane);
+
+  const char* src[PER_WAVE];
+#pragma unroll
+  for (int i = 0; i < PER_WAVE; ++i) {
+    const int j = wave + i * NW;
+    const int kc = j % KC, blk = j / KC;
+    const uint16_t* base;
+    if (blk < M * BR) {
+      const int m = blk / BR;
+      const int rt = min(rt0 + blk % BR, sg.row_tiles - 1);
+      base = (m == 0 ? sg.w[0] : sg.w[1]) + rt * strip;
+    } else {
+      const int lt = min(lt0 + blk - M * BR, g.lane_groups - 1);
+      base = g.x + lt * strip;
+    }
+    src[i] = reinterpret_cast<const char*>(base) + static_cast<int64_t>(kc) * kChunkBytes + foff;
+  }
+  auto issue = [&](int stage) {
+    u32x4* dst = ring + (stage % NS) * STAGE;
+#pragma unroll
+    for (int i = 0; i < PER_WAVE; ++i) {
+      const int j = wave + i * NW;
+      __builtin_amdgcn_global_load_lds(STRIDE_TC_GLOBAL(src[i] + static_cast<int64_t>(stage) * KC * kChunkBytes),
+                                       STRIDE_TC_LDS(dst + j * kWave), 16, 0, 0);
+    }
+  };
+
+  constexpr bool kPairStages = KC % 2 != 0;
+  f32x16 acc[M][PR][PL];
+  f32x16 y[HASY ? M : 1][HASY ? PR : 1][HASY ? PL : 1];
+  u32x4 fa[2][2][M][PR], fb[2][2][PL];  // [chunk parity][k half]
+  // This lane's piece inside a pair of tiles' chunks: tile (lane/16)%2 of the
+  // pair, 16x16x32 fragment slot (2h + lane/32)*16 + lane%16.
+  const int poff = ((lane >> 4) & 1) * KC * kWave + (lane >> 5) * 16 + (lane & 15);
+
+  auto read_frags = [&](int buf, int stage, int kc) {
+    const u32x4* stg = ring + (stage % NS) * STAGE + poff;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+      for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int p = 0; p < PR; ++p) fa[buf][h][m][p] = stg[((m * BR + wr * WRT + 2 * p) * KC + kc) * kWave + 32 * h];
+#pragma unroll
+      for (int q = 0; q < PL; ++q) fb[buf][h][q] = stg[((M * BR + wn * WLT + 2 * q) * KC + kc) * kWave + 32 * h];
+    }
+  };
+  auto sync_for = [&](int next) {
+    const int ahead = min(NS - 2, nst - 1 - next);
+    if (ahead >= NS - 2) __builtin_amdgcn_s_waitcnt(vm_lgkm0_imm((NS - 2) * PER_WAVE));
+    else if (ahead == 2) __builtin_amdgcn_s_waitcnt(vm_lgkm0_imm(2 * PER_WAVE));
+    else if (ahead == 1) __builtin_amdgcn_s_waitcnt(vm_lgkm0_imm(PER_WAVE));
+    else __builtin_amdgcn_s_waitcnt(vm_lgkm0_imm(0));
+    __builtin_amdgcn_s_barrier();
+  };
+
+#pragma unroll
+  for (int st = 0; st < NS; ++st)
+    if (st < nst) issue(st);
+  sync_for(0);
+  read_frags(0, 0, 0);
+
+  auto stage = [&](int i, auto parity) {
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc) {
+      const int cur = (decltype(parity)::value + kc) & 1, nxt = cur ^ 1;
+      __builtin_amdgcn_s_waitcnt(lgkm0_imm());
+      const bool last = kc + 1 == KC;
+      if (last && i + 1 < nst) {
+        sync_for(i + 1);
+        if (i + NS < nst) issue(i + NS);
+      }
+      read_frags(nxt, last ? min(i + 1, nst - 1) : i, last ? 0 : kc + 1);
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int q = 0; q < PL; ++q)
+#pragma unroll
+          for (int m = 0; m < M; ++m)
+#pragma unroll
+            for (int p = 0; p < PR; ++p) acc[m][p][q] = mfma32(fa[cur][h][m][p], fb[cur][h][q], acc[m][p][q]);
+      constexpr int kReads = 2 * (M * PR + PL), kMfma = 2 * M * PR * PL;
+      constexpr int kPer = kMfma / kReads > 0 ? kMfma / kReads : 1;
+#pragma unroll
+      for (int r = 0; r < kReads; ++r) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);     // one ds_read
+        __builtin_amdgcn_sched_group_barrier(0x008, kPer, 0);  // MFMAs
+      }
+    }
+  };
+
+  const int stages_per_split = per / KC;
+  int i = 0;
+  for (int s = 0; s < sg.splits; ++s) {
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+      for (int p = 0; p < PR; ++p)
+#pragma unroll
+        for (int q = 0; q < PL; ++q) {
+          if constexpr (Epi::kInitFromOutput) {
+            if (s == 0) {
+              f32x4 t[2][2];
+#pragma unroll
+              for (int a = 0; a < 2; ++a)
+#pragma unroll
+                for (int bb = 0; bb < 2; ++bb) {
+                  const int rt = rt0 + wr * WRT + 2 * p + a, lt = lt0 + wn * WLT + 2 * q + bb;
+                  t[a][bb] = rt < sg.row_tiles && lt < g.lane_groups ? Epi::init(o, rt, lt, lane) : f32x4{0.f, 0.f, 0.f, 0.f};
+                }
+              acc[m][p][q] = block_of_tiles(t, lane);
+              continue;
+            }
+          }
+          acc[m][p][q] = f32x16{};
+        }
+    if constexpr (kPairStages) {
+      for (int j = 0; j < stages_per_split; j += 2, i += 2) {
+        stage(i, std::integral_constant<int, 0>{});
+        stage(i + 1, std::integral_constant<int, 1>{});
+      }
+    } else {
+      for (int j = 0; j < stages_per_split; ++j, ++i) stage(i, std::integral_constant<int, 0>{});
+    }
+    if constexpr (HASY) {
+#pragma unroll
+      for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int p = 0; p < PR; ++p)
+#pragma unroll
+          for (int q = 0; q < PL; ++q) y[m][p][q] = s == 0 ? acc[m][p][q] : y[m][p][q] + acc[m][p][q];
+    }
+  }
+
+  auto block = [&](int m, int p, int q) -> const f32x16& {
+    if constexpr (HASY) return y[m][p][q];
+    else return acc[m][p][q];
+  };
+  if constexpr (Epi::kReduce) {
+    __syncthreads();  // the LDS ring is reused for the candidates
+    float* cand_v = reinterpret_cast<float*>(ring);
+    int32_t* cand_i = reinterpret_cast<int32_t*>(ring) + WM * BL * 16;
+    unroll<PL>([&](auto q) {
+      unroll<2>([&](auto bb) {
+        float bv = f32_of(0xFF800000u);
+        int32_t bi = -1;
+        unroll<PR>([&](auto p) {
+          unroll<2>([&](auto a) {
+            const f32x4 t = tile_of_block(block(0, p, q), a, bb, lane);
+            const int rt = rt0 + wr * WRT + 2 * p + a;
+            if (rt < sg.row_tiles) Epi::merge_tile(o, rt, t, lane, bv, bi);
+          });
+        });
+        const int l = 2 * q + bb;
+        if (lane < 16) {
+          cand_v[(wr * BL + wn * WLT + l) * 16 + lane] = bv;
+          cand_i[(wr * BL + wn * WLT + l) * 16 + lane] = bi;
+        }
+      });
+    });
+    __syncthreads();
+    if (wr == 0) {
+#pragma unroll
+      for (int l = 0; l < WLT; ++l) {
+        const int lt = lt0 + wn * WLT + l;
+        if (lt >= g.lane_groups) continue;
+        float v = f32_of(0xFF800000u);
+        int32_t ii = -1;
+#pragma unroll
+        for (int w = 0; w < WM; ++w)
+          arg_merge(v, ii, cand_v[(w * BL + wn * WLT + l) * 16 + (lane & 15)], cand_i[(w * BL + wn * WLT + l) * 16 + (lane & 15)]);
+        Epi::commit(o, g, lt, lane, v, ii, rb);
+      }
+    }
+    return;
+  }
+  unroll<PR>([&](auto p) {
+    unroll<PL>([&](auto q) {
+      unroll<2>([&](auto a) {
+        unroll<2>([&](auto bb) {
+          f32x4 t[M];
+#pragma unroll
+          for (int m = 0; m < M; ++m) t[m] = tile_of_block(block(m, p, q), a, bb, lane);
+          const int rt = rt0 + wr * WRT + 2 * p + a, lt = lt0 + wn * WLT + 2 * q + bb;
+          if (rt < sg.row_tiles && lt < g.lane_groups) Epi::apply(o, g, si, rt, lt, t, lane);
+        });
+      });
+    });
+  });
+}
+
 }  // namespace stride_tc

@@ -70,3 +70,82 @@ def mfma_equiv(a, b, c0, o16, o32, chunks: int, stream: int) -> None:
                                         c0.shape[0], chunks, stream)
     if rc:
         raise RuntimeError(f"stride_probe_mfma_equiv failed ({rc})")
+
+
+def _graph_time(torch, fns, side):
+    """Average seconds per call of fns (captured once in a HIP graph, replayed twice)."""
+    g = torch.cuda.CUDAGraph()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for f in fns:
+            f()
+    torch.cuda.current_stream().wait_stream(side)
+    with torch.cuda.graph(g):
+        for f in fns:
+            f()
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    g.replay()
+    g.replay()
+    e1.record()
+    e1.synchronize()
+    return e0.elapsed_time(e1) / 1e3 / (2 * len(fns))
+
+
+def main(argv=None) -> None:
+    """python -m stride_amd.probe [read] [strip] [mfma]: the floors the GEMM
+    kernels are judged against, as markdown table rows. Buffers rotate over up to
+    16 distinct copies in a 3 GiB pool, so the 256 MB MALL cannot serve repeats."""
+    import sys
+
+    import torch
+
+    what = set((argv if argv is not None else sys.argv[1:]) or ["read", "strip", "mfma"])
+    dev = "cuda:0"
+    side = torch.cuda.Stream()
+    out = torch.zeros(1 << 20, dtype=torch.int32, device=dev)
+    stream = lambda: torch.cuda.current_stream().cuda_stream
+    if what & {"read", "strip"}:
+        pool = torch.empty(3 << 30, dtype=torch.uint8, device=dev).fill_(1)
+    if "read" in what:
+        print("| bytes | best time | GB/s | grid | loads in flight |\n|---|---|---|---|---|", flush=True)
+        for mib in (8, 12, 32, 64, 128, 512):
+            nb = mib << 20
+            views = [pool[i * nb:(i + 1) * nb] for i in range(min(16, (3 << 30) // nb))]
+            best = None
+            for blocks in (256, 512, 1024, 2048, 4096, 0):
+                for unroll in (4, 8, 16):
+                    s = _graph_time(torch, [lambda v=v: read(v, out, blocks, unroll, stream()) for v in views], side)
+                    if best is None or s < best[0]:
+                        best = (s, blocks, unroll)
+            grid = "1 WG / 64 KiB" if best[1] == 0 else str(best[1])
+            print(f"| {mib} MiB | {best[0] * 1e6:.2f} us | {nb / best[0] / 1e9:.0f} | {grid} | {best[2]} |", flush=True)
+    if "strip" in what:
+        print("| bytes | strip | rotated starts | best time | GB/s |\n|---|---|---|---|---|", flush=True)
+        for mib in (64, 512):
+            nb = mib << 20
+            views = [pool[i * nb:(i + 1) * nb] for i in range(min(16, (3 << 30) // nb))]
+            for strip in (32768, 65536):
+                for rot in (0, 1):
+                    best = min(_graph_time(torch, [lambda v=v: strip_read(v, strip, out, blocks, unroll, rot, stream())
+                                                   for v in views], side)
+                               for blocks in (256, 512, 1024) for unroll in (8, 16))
+                    print(f"| {mib} MiB | {strip // 1024} KiB | {'yes' if rot else 'no'} | {best * 1e6:.2f} us | "
+                          f"{nb / best / 1e9:.0f} |", flush=True)
+    if "mfma" in what:
+        print("| form | waves per SIMD | TFLOP/s |\n|---|---|---|", flush=True)
+        fo = torch.zeros(1 << 16, dtype=torch.float32, device=dev)
+        iters = 4096
+        for blocks, label in ((256, "1"), (2048, "8")):
+            s = _graph_time(torch, [lambda: mfma_rate(fo, blocks, iters, stream())], side)
+            print(f"| 16x16x32, 8 accumulators | {label} | {blocks * 4 * iters * 8 * 16384 / s / 1e12:.0f} |", flush=True)
+            s = _graph_time(torch, [lambda: mfma_rate_variant(fo, blocks, iters, 1, stream())], side)
+            print(f"| 16x16x32, 16 accumulators | {label} | {blocks * 4 * iters * 16 * 16384 / s / 1e12:.0f} |", flush=True)
+            s = _graph_time(torch, [lambda: mfma_rate_variant(fo, blocks, iters, 2, stream())], side)
+            print(f"| 32x32x16, 4 accumulators | {label} | {blocks * 4 * iters * 4 * 32768 / s / 1e12:.0f} |", flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -9,7 +9,7 @@ adds a chunk twice. Every k-loop must therefore guard MFMAs with scalar
 fails if any MFMA is reachable, in straight-line order, after an EXEC
 narrowing with no `s_cbranch_execz` in between.
 
-Second check: every LDS-pipelined kernel (k_pipe) must use exactly the LDS of
+Second check: every LDS-pipelined kernel (k_pipe, k_pipe32) must use exactly the LDS of
 its staging ring, NS stages x (mats*WM*WRT + WN*WLT) tiles x KC chunks x 1 KiB.
 Anything more is a private copy the compiler moved into LDS (a local struct
 indexed at run time), which costs LDS capacity and an LDS round trip per use.
@@ -127,7 +127,7 @@ def test_pipe_lds_is_exactly_the_ring():
         kernels = kernel_lds(co)
     seen = 0
     for name, grp in kernels:
-        m = re.search(r"k_pipeINS_\d+(\w+?)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELb(\d)", name)
+        m = re.search(r"k_pipe(?:32)?INS_\d+(\w+?)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELb(\d)", name)
         if not m:
             continue
         wrt, wlt, wm, wn, kc, ns, _ = map(int, m.groups()[1:8])
