@@ -195,8 +195,9 @@ __device__ __forceinline__ const KvT* kv_row(const StrideKvRef& kv, int page_shi
 // the four query heads (an fmaf chain over the head dims in order, then times
 // scale); the page maximum is order-free; the exponentials follow. Each lane
 // then mixes the values of its dims over the positions in order; in the same
-// pass it adds the weights left to right, which yields the denominators (the
-// add and the mix see the weights in the same order) without a serial phase.
+// pass lane h < 4 adds head h's weights left to right (one LDS word per
+// position), which yields the denominators without a serial phase and without
+// every lane repeating the four adds.
 // KvT is uint16_t (bf16 KV, the tensor-core path) or float (the exact path);
 // the arithmetic is the same, on the widened values.
 template <int D, class KvT>
@@ -276,9 +277,13 @@ __global__ __launch_bounds__(64) void k_attn_page(StrideAttentionParams p, int p
   __syncthreads();
   float* rec = p.scratch + (static_cast<int64_t>(j * p.n_kv + g) * p.max_pages + page) * p.rec_floats;
   float* v_out = rec + 8;
+  const float* wflat = reinterpret_cast<const float*>(w4);
+  float den = 0.0f;  // head (lane & 3)
 #pragma unroll
-  for (int d = lane; d < D; d += 64) {
-    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f}, den = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int it = 0; it < (D + 63) / 64; ++it) {
+    const int d = lane + 64 * it;
+    if (d >= D) continue;
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll 4
     for (int i = 0; i < n; ++i) {
       float v;
@@ -286,20 +291,15 @@ __global__ __launch_bounds__(64) void k_attn_page(StrideAttentionParams p, int p
       else v = vs[i][d];
       const f32x4 wi = w4[i];
 #pragma unroll
-      for (int h = 0; h < kHeadsPerGroup; ++h) {
-        acc[h] = __builtin_fmaf(wi[h], v, acc[h]);
-        den[h] = den[h] + wi[h];
-      }
+      for (int h = 0; h < kHeadsPerGroup; ++h) acc[h] = __builtin_fmaf(wi[h], v, acc[h]);
+      if (it == 0) den = den + wflat[i * kHeadsPerGroup + (lane & 3)];
     }
 #pragma unroll
     for (int h = 0; h < kHeadsPerGroup; ++h) v_out[h * D + d] = acc[h];
-    if (d == 0) {
-#pragma unroll
-      for (int h = 0; h < kHeadsPerGroup; ++h) {
-        rec[h] = mx[h];
-        rec[4 + h] = den[h];
-      }
-    }
+  }
+  if (lane < kHeadsPerGroup) {
+    rec[lane] = mx[lane];
+    rec[4 + lane] = den;
   }
 }
 
