@@ -1,7 +1,7 @@
 """Benchmark: the Llama-3.2-1B decode-step GEMM set on one MI355X.
 
 A "step" is one decode step's worth of linear layers for a batch of M rows
-(BASELINE config 2 + config 3): for each of 16 layers, fused QKV (N=3072, K=2048,
+(the decode GEMM set and the LM head): for each of 16 layers, fused QKV (N=3072, K=2048,
 RoPE + bf16 KV append), O + residual (2048 x 2048), gate+up + SiLU (2 x 8192 x
 2048) and down + residual (2048 x 8192), then the LM head with greedy argmax
 (128256 x 2048). Weights are random-init bf16 ~N(0, 0.02) in the reference tile
@@ -50,7 +50,7 @@ def parse():
     ap.add_argument("--engine-only", type=int, default=0,
                     help="run only the full decode step (for kernel profiles of it) and print its JSON")
     ap.add_argument("--engine", type=int, default=1,
-                    help="also time one full decode step of the config-5 engine (0 to skip)")
+                    help="also time one full decode step of the engine (0 to skip)")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="also run one plain device copy of this size (calibrates FETCH_SIZE/WRITE_SIZE counters)")
     return ap.parse_args()
@@ -257,7 +257,7 @@ def cpu_baseline(seconds, threads):
 
 
 def engine_step(torch, dev, m, steps, warmup, position=383):
-    """BASELINE config 5's decode step at batch m: the whole step of
+    """The full greedy decode step at batch m: the whole step of
     stride_amd.engine (embedding, per layer RMSNorm, QKV + RoPE + KV append,
     paged attention over `position` + 1 positions, O, RMSNorm, gate/up, down;
     final RMSNorm and the greedy LM head), every row at `position` (the middle of

@@ -8,7 +8,7 @@ tc_lm_greedy. Rows are (slot, position, token) triples; prompts are processed as
 ordinary rows (chunked prefill), so a prompt token and a decode token go through
 identical arithmetic. Every row's result depends only on its own slot contents
 and position, never on the batch it shares a step with, its lane, or where its
-KV pages live; the config-5 test runs sequences alone and in shuffled batches
+KV pages live; the full-step engine test runs sequences alone and in shuffled batches
 and compares their token streams and fingerprints.
 
 Each sequence keeps the reference scheduler's fingerprint (src/scheduler.cpp:

@@ -1,4 +1,4 @@
-"""BASELINE config 5 on one GPU: a greedy decode of a random-init
+"""The full greedy decode on one GPU: a greedy decode of a random-init
 Llama-3.2-1B-shaped model (16 layers, hidden 2048, 32/8 heads, FFN 8192,
 vocab 128256, 16-token KV pages) through every tensor-core operator. Each
 sequence's generated tokens, the fp32 bits of their logits and the scheduler

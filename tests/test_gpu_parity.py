@@ -62,7 +62,7 @@ def test_config1_projection(exact, m):
 
 @pytest.mark.parametrize("m", [1, 37])
 def test_config1_projection_fp32_x(exact, m):
-    """Config 1 as BASELINE states it: x fp32 ~N(0,1) (not bf16-representable),
+    """The single-projection CPU-comparison case: x fp32 ~N(0,1) (not bf16-representable),
     y = x W^T, N=K=2048, seed 0, through stride_tc_gemm_f32x, against the CPU exact
     path on the same fp32 x; the rows must not depend on M."""
     n = k = 2048
