@@ -19,7 +19,8 @@ from concurrent.futures import ThreadPoolExecutor
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_obj")
-SOURCES = [os.path.join(CSRC, "tc_gemm.hip"), os.path.join(CSRC, "tc_aux.hip"), os.path.join(CSRC, "exact.hip")]
+SOURCES = [os.path.join(CSRC, f) for f in ("tc_gemm.hip", "tc_gemm_mlp13.hip", "tc_gemm_qkv.hip", "tc_gemm_lm_full.hip",
+                                            "tc_gemm_lm_greedy.hip", "tc_aux.hip", "exact.hip")]
 OUT = os.path.join(HERE, "libstride_tc.so")
 PROBE_SOURCES = [os.path.join(CSRC, "probe.hip")]
 PROBE_OUT = os.path.join(HERE, "libstride_probe.so")

@@ -199,7 +199,8 @@ struct EpiArgmax {  // per-lane greedy argmax  (src/kernels_tc.cu:590-630)
 // Second pass of the greedy LM head: lane j reduces the candidates of all nrb
 // row blocks (any order gives the same lexicographic max) and merges the winner
 // into best[j] (the caller's initial entry takes part, as in the reference).
-__global__ __launch_bounds__(256) void k_argmax_finish(const unsigned long long* __restrict__ cand, int nrb, int rows,
+// Internal linkage: every translation unit that includes this header gets its own copy.
+static __global__ __launch_bounds__(256) void k_argmax_finish(const unsigned long long* __restrict__ cand, int nrb, int rows,
                                                        StrideBestEntry* best) {
   const int j = blockIdx.x;
   float bv = f32_of(0xFF800000u);

@@ -31,24 +31,9 @@
 // All call the same chunk order, the same MFMA instruction and the same
 // epilogue functions, so every output row has the same bits for any M and any
 // configuration; run() picks the configuration from measured sweeps.
-#include <hip/hip_runtime.h>
-
-#include <cstdio>
-#include <cstddef>
-#include <algorithm>
-#include <cstring>
-#include <string>
-
-#include "tc_dec.hpp"
-#include "tc_epilogue.hpp"
-#include "tc_pipe.hpp"
-#include "tc_stream.hpp"
-#include "tc_tile.hpp"
+#include "tc_gemm_run.hpp"
 
 namespace stride_tc {
-
-// ---------------------------------------------------------------------------
-// Host side: split rule, validation, launch selection.
 
 thread_local std::string g_last_error;
 
@@ -57,128 +42,13 @@ int fail(int code, const std::string& msg) {
   return code;
 }
 
-// The fixed K-split for an N x K weight matrix. Matrices with few row tiles
-// (N <= 4096: Q, K, V, output, down) get 8 splits so that a decode launch has
-// enough independent weight streams; gate/up (N <= 16384) get 2; the LM head
-// gets 1. S is then capped by the chunk count and halved until it divides it.
-int split_count(int n, int k) {
-  const int chunks = k / kChunkCols;
-  int s = n <= 4096 ? 8 : (n <= 16384 ? 2 : 1);
-  if (s > chunks) s = chunks;
-  while (s > 1 && chunks % s != 0) s >>= 1;
-  return s < 1 ? 1 : s;
-}
-
-bool lanes_ok(const StrideLanes& l, std::string& why) {
-  if (l.rows < 0 || l.lane_groups != (l.rows + 15) / 16) {
-    why = "lane_groups must equal ceil(rows / 16) (rows=" + std::to_string(l.rows) +
-          ", lane_groups=" + std::to_string(l.lane_groups) + ")";
-    return false;
-  }
-  return true;
-}
-
-bool mat_ok(const StrideGemmMat& m, const char* name, std::string& why) {
-  if (!m.w || m.groups <= 0 || m.cols <= 0 || m.cols % kChunkCols != 0) {
-    why = std::string(name) + ": need a weight pointer, groups > 0 and cols a positive multiple of 32 (groups=" +
-          std::to_string(m.groups) + ", cols=" + std::to_string(m.cols) + ")";
-    return false;
-  }
-  return true;
-}
-
-// Decode-regime configurations of k_stream: (R row tiles per wave, LT lane tiles,
-// WS split waves, WR row waves, U chunks per batch, XL x staged in LDS, XS one
-// split per workgroup, the last arriving workgroup of a tile group combining). Which
-// one runs never changes results: all evaluate the same chunk order and the same
-// split combine. The table is indexed by stride_tc_set_stream_config() for tuning
-// sweeps and by pick_decode() otherwise.
-#define STRIDE_TC_DECODE_CONFIGS(S) \
-  S(0, 1, 1, 8, 1, 8, false, false) \
-  S(1, 1, 1, 8, 1, 4, false, false) \
-  S(2, 1, 1, 2, 4, 8, false, false) \
-  S(3, 1, 1, 1, 8, 8, false, false) \
-  S(4, 1, 1, 1, 4, 8, false, false) \
-  S(5, 1, 2, 8, 1, 8, false, false) \
-  S(6, 1, 2, 2, 4, 8, false, false) \
-  S(7, 1, 2, 1, 8, 8, false, false) \
-  S(8, 1, 4, 8, 1, 4, false, false) \
-  S(9, 2, 4, 8, 1, 2, false, false) \
-  S(10, 1, 4, 2, 4, 4, false, false) \
-  S(11, 1, 4, 2, 4, 2, true, false) \
-  S(12, 1, 4, 1, 8, 4, false, false) \
-  S(13, 2, 4, 1, 8, 2, true, false) \
-  S(14, 1, 8, 8, 1, 2, false, false) \
-  S(15, 2, 8, 8, 1, 2, false, false) \
-  S(16, 1, 8, 1, 8, 2, true, false) \
-  S(17, 1, 8, 1, 8, 2, false, false) \
-  S(18, 1, 1, 16, 1, 4, false, false) \
-  S(19, 1, 1, 16, 1, 8, false, false) \
-  S(20, 1, 2, 16, 1, 4, false, false) \
-  S(21, 1, 4, 16, 1, 2, false, false) \
-  S(22, 1, 2, 4, 2, 4, false, false) \
-  S(23, 1, 1, 4, 2, 8, false, false) \
-  S(24, 1, 4, 4, 2, 4, false, false) \
-  S(25, 1, 2, 16, 1, 2, false, false) \
-  S(26, 1, 1, 16, 1, 2, false, false) \
-  S(27, 2, 4, 8, 1, 4, false, false) \
-  S(28, 2, 8, 8, 1, 1, false, false) \
-  S(29, 4, 4, 8, 1, 1, false, false) \
-  S(30, 4, 8, 8, 1, 1, false, false) \
-  S(31, 2, 8, 8, 2, 1, true, false) \
-  S(32, 1, 8, 8, 2, 1, true, false) \
-  S(33, 2, 2, 8, 1, 4, false, false) \
-  S(34, 1, 1, 8, 2, 8, false, false) \
-  S(35, 2, 1, 8, 1, 8, false, false) \
-  S(36, 1, 4, 2, 4, 8, true, false) \
-  S(37, 1, 8, 2, 4, 8, true, false) \
-  S(38, 2, 4, 2, 4, 8, true, false) \
-  S(39, 1, 8, 1, 8, 4, true, false) \
-  S(40, 2, 8, 1, 8, 4, true, false) \
-  S(41, 1, 4, 2, 8, 8, true, false) \
-  S(42, 2, 8, 2, 4, 4, true, false) \
-  S(43, 1, 8, 1, 4, 8, true, true) \
-  S(44, 2, 8, 1, 4, 4, true, true) \
-  S(45, 1, 8, 1, 8, 8, true, true) \
-  S(46, 1, 8, 1, 2, 4, true, true) \
-  S(47, 1, 4, 1, 4, 8, true, true) \
-  S(48, 2, 4, 1, 4, 4, true, true) \
-  S(49, 1, 8, 1, 4, 4, true, true) \
-  S(50, 2, 8, 1, 2, 4, true, true) \
-  S(51, 4, 8, 1, 2, 2, true, true) \
-  S(52, 2, 8, 1, 4, 2, true, true) \
-  S(53, 1, 1, 1, 4, 8, false, true) \
-  S(54, 1, 1, 1, 8, 8, false, true) \
-  S(55, 1, 1, 1, 2, 8, false, true) \
-  S(56, 2, 1, 1, 4, 4, false, true) \
-  S(57, 1, 2, 1, 4, 8, false, true) \
-  S(58, 1, 8, 1, 4, 8, false, true)
-
-struct DecodeCfg {
-  int r, lt, ws, wr, u;
-  bool xl, xs;
-};
-
-#define STRIDE_TC_ROW(i, R, LT, WS, WR, U, XL, XS) {R, LT, WS, WR, U, XL, XS},
-constexpr DecodeCfg kDecodeCfgs[] = {STRIDE_TC_DECODE_CONFIGS(STRIDE_TC_ROW)};
-#undef STRIDE_TC_ROW
-constexpr int kNumDecodeCfgs = sizeof(kDecodeCfgs) / sizeof(kDecodeCfgs[0]);
-
-int g_forced_cfg = -1;
-
-// Device scratch shared by two uses: the greedy LM head's argmax candidates
-// (one 8-byte (value, index) slot per (row block, batch lane)) and the fp32
-// split partials of cross-workgroup split launches. A fixed file-scope device
-// array, so the entry points allocate nothing; launches on one device share it
-// and must be ordered on one stream (the reference keeps every launch on one
-// stream, src/kernels.cu:457-460).
-constexpr int64_t kScratchBytes = int64_t{16} << 20;
-constexpr int64_t kCandSlots = kScratchBytes / 8;
+// One device scratch array (partials of cross-workgroup split launches or the
+// greedy LM head's candidates) and the split arrival counters; their addresses
+// come from hipGetSymbolAddress once per device, so no entry point allocates.
 __device__ __align__(256) unsigned long long g_scratch[kScratchBytes / 8];
 
 // Arrival counters of cross-workgroup split launches, one per (row block, lane
 // group) unit; each launch leaves them at zero.
-constexpr int kSplitUnits = 1 << 16;
 __device__ __align__(256) int32_t g_split_cnt[kSplitUnits];
 
 int32_t* split_counters() {
@@ -204,452 +74,11 @@ unsigned long long* scratch_base() {
   }
   return cache[dev];
 }
-int g_last_cfg = -1;  // configuration of the last decode-regime launch (-2: prefill kernel)
 
-template <class Epi, int R, int LT, int WS, int WR, int U, bool XL, bool XS>
-void launch_stream(Geometry g, const typename Epi::Out& o, hipStream_t st) {
-  if constexpr (XS && Epi::kReduce) {
-    return;  // never selected (decode_cfg_fits)
-  } else {
-    int blocks = 0;
-    for (int i = 0; i < g.nseg; ++i) {
-      g.seg[i].blocks = (g.seg[i].row_tiles + WR * R - 1) / (WR * R);
-      blocks += XS ? g.seg[i].blocks * g.seg[i].splits : g.seg[i].blocks;
-    }
-    blocks *= (g.lane_groups + LT - 1) / LT;
-    hipLaunchKernelGGL((k_stream<Epi, R, LT, WS, WR, U, XL, XS>), dim3(blocks), dim3(kWave * WS * WR), 0, st, g, o);
-  }
-}
-
-template <class Epi>
-void launch_decode_cfg(int idx, const Geometry& g, const typename Epi::Out& o, hipStream_t st) {
-  switch (idx) {
-#define STRIDE_TC_CASE(i, R, LT, WS, WR, U, XL, XS)          \
-  case i:                                                    \
-    launch_stream<Epi, R, LT, WS, WR, U, XL, XS>(g, o, st); \
-    break;
-    STRIDE_TC_DECODE_CONFIGS(STRIDE_TC_CASE)
-#undef STRIDE_TC_CASE
-    default:
-      break;
-  }
-}
-
-// Output tiles of a launch (all segments).
-int64_t total_tiles(const Geometry& g) {
-  int64_t t = 0;
-  for (int i = 0; i < g.nseg; ++i) t += static_cast<int64_t>(g.seg[i].row_tiles) * g.lane_groups;
-  return t;
-}
-
-// Can configuration c serve this launch?
-bool decode_cfg_fits(const DecodeCfg& c, Geometry g, int smax, int mats, bool reduce) {
-  int u = c.u / mats > 0 ? c.u / mats : 1;
-  if (c.xl) {
-    const int umax = 128 / (c.ws * 2 * c.lt) > 0 ? 128 / (c.ws * 2 * c.lt) : 1;
-    u = u < umax ? u : umax;  // as k_stream clamps it
-  }
-  const int chunks = g.col_tiles >> 1;
-  if (c.xs) {
-    if (reduce || c.ws != 1 || smax < 2 || smax > kMaxXSplits) return false;
-    if (total_tiles(g) * smax * mats * 1024 > kScratchBytes) return false;
-    int64_t units = 0;
-    for (int i = 0; i < g.nseg; ++i) units += (g.seg[i].row_tiles + c.wr * c.r - 1) / (c.wr * c.r);
-    if (units * ((g.lane_groups + c.lt - 1) / c.lt) > kSplitUnits) return false;
-    if (c.xl && (u * c.lt) % c.wr == 0)
-      for (int i = 0; i < g.nseg; ++i)
-        if ((chunks / g.seg[i].splits) % u != 0) return false;
-    return true;
-  }
-  if (c.ws < smax) return false;
-  if (c.xl && (u * c.lt) % c.wr == 0) {
-    for (int i = 0; i < g.nseg; ++i)
-      if (g.seg[i].splits != c.ws || (chunks / g.seg[i].splits) % u != 0) return false;
-  }
-  return true;
-}
-
-// Configurations of k_dec (weights to registers, activations through an LDS
-// ring): (R row tiles per wave, LT lane tiles, NW waves, KC chunks per stage,
-// NSS ring slots, XS one split per workgroup, WS split groups per workgroup, OCC
-// workgroups per CU the register allocation is bounded for). Index 1000 + i in the tuning hook
-// selects configuration i.
-#define STRIDE_TC_DEC_CONFIGS(D)       \
-  D(0, 1, 8, 4, 2, 4, true, 1, 1)     \
-  D(1, 1, 8, 4, 1, 8, true, 1, 1)     \
-  D(2, 1, 8, 8, 2, 4, true, 1, 1)     \
-  D(3, 1, 8, 4, 2, 4, false, 2, 1)    \
-  D(4, 1, 8, 4, 2, 4, false, 1, 1)    \
-  D(5, 2, 8, 4, 2, 4, false, 1, 1)    \
-  D(6, 1, 4, 4, 2, 4, true, 1, 1)     \
-  D(7, 1, 4, 4, 1, 8, true, 1, 1)     \
-  D(8, 2, 4, 4, 2, 4, false, 1, 1)    \
-  D(9, 1, 8, 4, 1, 8, false, 2, 1)    \
-  D(10, 1, 4, 4, 2, 4, false, 1, 1)   \
-  D(11, 1, 4, 4, 2, 4, false, 2, 1)   \
-  D(12, 2, 8, 4, 1, 4, false, 1, 2)   \
-  D(13, 1, 4, 4, 1, 8, false, 2, 1)   \
-  D(14, 2, 8, 4, 1, 8, false, 1, 1)   \
-  D(15, 1, 2, 2, 2, 4, true, 1, 1)    \
-  D(16, 1, 8, 4, 1, 4, false, 1, 2)   \
-  D(17, 2, 8, 4, 1, 6, false, 1, 2)   \
-  D(18, 2, 4, 4, 2, 4, false, 1, 2)   \
-  D(19, 4, 4, 4, 1, 4, false, 1, 2)   \
-  D(20, 1, 8, 4, 1, 4, false, 2, 2)   \
-  D(21, 2, 8, 8, 1, 4, false, 1, 1)
-
-struct DecCfg {
-  int r, lt, nw, kc, nss;
-  bool xs;
-  int ws, occ;
-};
-#define STRIDE_TC_DEC_ROW(i, R, LT, NW, KC, NSS, XS, WS, OCC) {R, LT, NW, KC, NSS, XS, WS, OCC},
-constexpr DecCfg kDecCfgs[] = {STRIDE_TC_DEC_CONFIGS(STRIDE_TC_DEC_ROW)};
-#undef STRIDE_TC_DEC_ROW
-constexpr int kNumDecCfgs = sizeof(kDecCfgs) / sizeof(kDecCfgs[0]);
-constexpr int kDecIndexBase = 1000;
+int g_forced_cfg = -1;
 int g_forced_dec = -1;
-
-bool dec_cfg_fits(const DecCfg& c, const Geometry& g, int smax, int mats, bool reduce) {
-  const int chunks = g.col_tiles >> 1;
-  if (c.xs) {
-    if (reduce || smax < 2 || smax > kMaxXSplits) return false;
-    if (total_tiles(g) * smax * mats * 1024 > kScratchBytes) return false;
-    int64_t units = 0;
-    for (int i = 0; i < g.nseg; ++i) units += (g.seg[i].row_tiles + c.nw * c.r - 1) / (c.nw * c.r);
-    if (units * ((g.lane_groups + c.lt - 1) / c.lt) > kSplitUnits) return false;
-  } else {
-    if (reduce && c.ws != 1) return false;
-    for (int i = 0; i < g.nseg; ++i)
-      if (g.seg[i].splits != c.ws) return false;
-  }
-  for (int i = 0; i < g.nseg; ++i) {
-    const int per = chunks / g.seg[i].splits;
-    if (per % c.kc != 0 || (per / c.kc) % c.nss != 0) return false;
-  }
-  return true;
-}
-
-template <class Epi, int R, int LT, int NW, int KC, int NSS, bool XS, int WS, int OCC>
-void launch_dec(Geometry g, const typename Epi::Out& o, hipStream_t st) {
-  if constexpr ((XS || WS > 1) && Epi::kReduce) {
-    return;  // never selected (dec_cfg_fits)
-  } else {
-    constexpr int NR = NW / WS;
-    int blocks = 0;
-    for (int i = 0; i < g.nseg; ++i) {
-      g.seg[i].blocks = (g.seg[i].row_tiles + NR * R - 1) / (NR * R);
-      blocks += XS ? g.seg[i].blocks * g.seg[i].splits : g.seg[i].blocks;
-    }
-    blocks *= (g.lane_groups + LT - 1) / LT;
-    hipLaunchKernelGGL((k_dec<Epi, R, LT, NW, KC, NSS, XS, WS, OCC>), dim3(blocks), dim3(kWave * NW), 0, st, g, o);
-  }
-}
-
-template <class Epi>
-void launch_dec_cfg(int idx, const Geometry& g, const typename Epi::Out& o, hipStream_t st) {
-  switch (idx) {
-#define STRIDE_TC_DEC_CASE(i, R, LT, NW, KC, NSS, XS, WS, OCC) \
-  case i:                                                       \
-    launch_dec<Epi, R, LT, NW, KC, NSS, XS, WS, OCC>(g, o, st); \
-    break;
-    STRIDE_TC_DEC_CONFIGS(STRIDE_TC_DEC_CASE)
-#undef STRIDE_TC_DEC_CASE
-    default:
-      break;
-  }
-}
-
-// Default choice by lane-tile count, split count, segment count and split
-// length, from measured sweeps on MI355X (HIP-graph timing, weights rotated past
-// the MALL).
-int pick_decode(int T, int smax, int mats, int nseg, int per) {
-  (void)mats;
-  if (smax > 8) return T <= 1 ? 18 : (T <= 2 ? 20 : 21);
-  if (T <= 1) {
-    if (smax == 1) return 4;
-    if (smax == 2) return 34;
-    return nseg == 1 && per >= 32 ? 53 : 0;  // long splits: one split per workgroup
-  }
-  if (T <= 2) return smax == 1 ? 7 : (smax == 2 ? 22 : 1);
-  if (T <= 4) return smax == 1 ? 13 : (smax == 2 ? 27 : (nseg == 3 ? 33 : 5));
-  return smax == 1 ? 16 : (smax == 2 ? 36 : (nseg == 3 ? 9 : 33));
-}
-
-template <class Epi, int WRT, int WLT>
-int launch_tile(Geometry g, const typename Epi::Out& o, hipStream_t st) {
-  int blocks = 0;
-  for (int i = 0; i < g.nseg; ++i) {
-    g.seg[i].blocks = (g.seg[i].row_tiles + 2 * WRT - 1) / (2 * WRT);
-    blocks += g.seg[i].blocks;
-  }
-  blocks *= (g.lane_groups + 2 * WLT - 1) / (2 * WLT);
-  hipLaunchKernelGGL((k_tile<Epi, WRT, WLT>), dim3(blocks), dim3(256), 0, st, g, o);
-  return 0;
-}
-
-template <class Epi, int WRT, int WLT, int WM, int WN, int KC, int NS, int OCC, int MF32 = 0>
-void launch_pipe(Geometry g, const typename Epi::Out& o, int smax, hipStream_t st) {
-  constexpr int BR = WM * WRT, BL = WN * WLT;
-  int blocks = 0;
-  for (int i = 0; i < g.nseg; ++i) {
-    g.seg[i].blocks = (g.seg[i].row_tiles + BR - 1) / BR;
-    blocks += g.seg[i].blocks;
-  }
-  blocks *= (g.lane_groups + BL - 1) / BL;
-  if constexpr (MF32) {
-    if (smax > 1)
-      hipLaunchKernelGGL((k_pipe32<Epi, WRT, WLT, WM, WN, KC, NS, OCC, true>), dim3(blocks), dim3(kWave * WM * WN), 0, st, g, o);
-    else
-      hipLaunchKernelGGL((k_pipe32<Epi, WRT, WLT, WM, WN, KC, NS, OCC, false>), dim3(blocks), dim3(kWave * WM * WN), 0, st, g, o);
-  } else {
-    if (smax > 1)
-      hipLaunchKernelGGL((k_pipe<Epi, WRT, WLT, WM, WN, KC, NS, OCC, true>), dim3(blocks), dim3(kWave * WM * WN), 0, st, g, o);
-    else
-      hipLaunchKernelGGL((k_pipe<Epi, WRT, WLT, WM, WN, KC, NS, OCC, false>), dim3(blocks), dim3(kWave * WM * WN), 0, st, g, o);
-  }
-}
-
-// Prefill configurations of k_pipe: (WRT, WLT, WM, WN, KC, NS, OCC, MF32). For
-// the paired gate/up GEMM WRT counts pairs and is halved (two matrices per row
-// tile). MF32 = 1 runs k_pipe32 (32x32x16 MFMAs; same bits).
-// Index -3 - i in the tuning hook selects configuration i.
-#define STRIDE_TC_PIPE_CONFIGS(X) \
-  X(0, 4, 4, 2, 2, 2, 3, 1, 0) \
-  X(1, 4, 4, 4, 2, 2, 2, 1, 0) \
-  X(2, 4, 4, 2, 4, 2, 2, 1, 0) \
-  X(3, 8, 4, 2, 4, 2, 2, 1, 0) \
-  X(4, 4, 8, 4, 2, 2, 2, 1, 0) \
-  X(5, 4, 8, 2, 2, 2, 3, 1, 0) \
-  X(6, 4, 4, 4, 4, 2, 2, 1, 0) \
-  X(7, 8, 4, 2, 2, 2, 3, 1, 0) \
-  X(8, 4, 4, 4, 2, 2, 3, 1, 0) \
-  X(9, 4, 8, 2, 2, 2, 2, 1, 0) \
-  X(10, 4, 2, 1, 4, 2, 4, 1, 0) \
-  X(11, 4, 4, 1, 2, 2, 4, 1, 0) \
-  X(12, 2, 2, 2, 4, 2, 4, 1, 0) \
-  X(13, 2, 4, 1, 2, 2, 4, 1, 0) \
-  X(14, 4, 1, 1, 4, 2, 4, 1, 0) \
-  X(15, 2, 2, 1, 4, 2, 4, 2, 0) \
-  X(16, 4, 2, 2, 2, 2, 4, 1, 0) \
-  X(17, 4, 1, 1, 4, 2, 6, 1, 0) \
-  X(18, 4, 8, 4, 2, 1, 4, 1, 0) \
-  X(19, 4, 8, 4, 2, 1, 5, 1, 0) \
-  X(20, 8, 4, 2, 4, 1, 4, 1, 0) \
-  X(21, 4, 4, 4, 2, 1, 5, 1, 0) \
-  X(22, 4, 4, 4, 2, 1, 6, 1, 0) \
-  X(23, 4, 4, 2, 4, 1, 5, 1, 0) \
-  X(24, 8, 8, 2, 2, 1, 4, 1, 0) \
-  X(25, 4, 8, 2, 2, 1, 6, 1, 0) \
-  X(26, 4, 4, 4, 2, 2, 3, 1, 1) \
-  X(27, 4, 4, 2, 4, 1, 5, 1, 1)
-
-constexpr int kNumPipeCfgs = 28;
 int g_forced_pipe = -1;
-
-template <class Epi>
-void launch_pipe_cfg(int idx, const Geometry& g, const typename Epi::Out& o, int smax, hipStream_t st) {
-  switch (idx) {
-#define STRIDE_TC_PIPE_CASE(i, WRT, WLT, WM, WN, KC, NS, OCC, MF)                                                 \
-  case i:                                                                                                         \
-    launch_pipe<Epi, (Epi::kMats == 2 ? (WRT > 2 ? WRT / 2 : WRT) : WRT), WLT, WM, WN, KC, NS, OCC, MF>(g, o, smax, st); \
-    break;
-    STRIDE_TC_PIPE_CONFIGS(STRIDE_TC_PIPE_CASE)
-#undef STRIDE_TC_PIPE_CASE
-    default:
-      break;
-  }
-}
-
-// Default prefill configuration (from measured sweeps): 256-row x 256-lane tiles
-// (8 waves of 4x8) when there are no K splits to carry and enough row tiles;
-// 256 x 128 (8 waves of 4x4, splits folded in registers) when the grid still
-// fills the CUs; 128 x 128 (4 waves) for small matrices.
-int pick_pipe(const Geometry& g, int smax) {
-  int rows = 0;
-  for (int i = 0; i < g.nseg; ++i) rows += g.seg[i].row_tiles;
-  if (smax == 1 && rows >= 512) return 4;
-  const int blocks_256x128 = ((rows + 15) / 16) * ((g.lane_groups + 7) / 8);
-  return blocks_256x128 >= 256 ? 8 : 0;
-}
-
-bool pipe_cfg_fits(int idx, const Geometry& g) {
-  static const int kc[] = {
-#define STRIDE_TC_PIPE_KC(i, WRT, WLT, WM, WN, KC, NS, OCC, MF) KC,
-      STRIDE_TC_PIPE_CONFIGS(STRIDE_TC_PIPE_KC)
-#undef STRIDE_TC_PIPE_KC
-  };
-  const int chunks = g.col_tiles >> 1;
-  // An odd chunk count per stage is processed two stages at a time.
-  const int step = kc[idx] % 2 ? 2 * kc[idx] : kc[idx];
-  for (int i = 0; i < g.nseg; ++i)
-    if ((chunks / g.seg[i].splits) % step != 0) return false;
-  return true;
-}
-
-// Largest lane-tile count served by the streaming kernel.
-constexpr int kStreamMaxLaneTiles = 8;
-
-// Row tiles per workgroup of prefill configuration idx.
-int pipe_rows_per_block(int idx, int mats) {
-  static const int wrt[] = {
-#define STRIDE_TC_PIPE_WRT(i, WRT, WLT, WM, WN, KC, NS, OCC, MF) WRT,
-      STRIDE_TC_PIPE_CONFIGS(STRIDE_TC_PIPE_WRT)
-#undef STRIDE_TC_PIPE_WRT
-  };
-  static const int wm[] = {
-#define STRIDE_TC_PIPE_WM(i, WRT, WLT, WM, WN, KC, NS, OCC, MF) WM,
-      STRIDE_TC_PIPE_CONFIGS(STRIDE_TC_PIPE_WM)
-#undef STRIDE_TC_PIPE_WM
-  };
-  const int r = mats == 2 && wrt[idx] > 2 ? wrt[idx] / 2 : wrt[idx];  // as launch_pipe_cfg halves it
-  return wm[idx] * r;
-}
-
-// Automatic choice of kernel family and configuration, from measured sweeps on
-// MI355X (HIP-graph timing, weights rotated past the MALL; every choice computes
-// the same bits). kind 0: k_stream configuration, kind 1: k_pipe configuration,
-// kind 3: k_dec configuration.
-struct Pick {
-  int kind, idx;
-};
-
-// At most 8 lane tiles. At three or four lane tiles the register-streamed
-// kernel with an activation ring wins for the LM head and (two split groups per
-// workgroup) for the paired gate/up GEMM; otherwise the LDS-pipelined kernel
-// with small blocks wins for the LM head from two lane tiles up and for gate/up
-// from three.
-Pick pick_small(int T, int smax, int mats, int nseg, int per) {
-  if (smax == 1 && T >= 3 && T <= 4) return {3, 8};
-  if (smax == 1 && T >= 2) return {1, T <= 4 ? 14 : 8};
-  if (smax == 2 && mats == 2 && T >= 3 && T <= 4) return {3, 13};
-  if (smax == 2 && mats == 2 && T >= 3) return {1, 15};
-  return {0, pick_decode(T, smax, mats, nseg, per)};
-}
-
-// More than 8 lane tiles. Matrices with eight splits (QKV, O, down) have few row
-// tiles and long split chains: up to a few hundred rows the streaming kernel,
-// whose waves run the splits side by side, beats the pipeline, which walks them
-// one after another; beyond, the pipeline with a block shape per size.
-Pick pick_large(const Geometry& g, int T, int smax, int per) {
-  if (smax == 1) return {1, T <= 12 || T > 24 ? 3 : 8};
-  if (smax == 2) {
-    if (T <= 12) return {1, 12};
-    if (T <= 24) return {1, 8};
-    if (T <= 48) return {1, 2};
-    return {1, pick_pipe(g, smax)};
-  }
-  if (g.nseg == 3) {  // fused QKV
-    if (T <= 12) return {0, 33};
-    if (T <= 24) return {0, 29};
-    if (T <= 64) return {1, 12};
-    return {1, 2};
-  }
-  if (per >= 32) {  // long splits (down)
-    if (T <= 12) return {0, 27};
-    if (T <= 32) return {0, 29};
-    if (T <= 64) return {0, 30};
-    return {1, pick_pipe(g, smax)};
-  }
-  if (T <= 12) return {0, 27};
-  if (T <= 32) return {0, 29};
-  if (T <= 64) return {1, 12};
-  if (T <= 96) return {1, 14};
-  if (T <= 128) return {1, 0};
-  return {1, 2};
-}
-
-template <class Epi>
-int run(Geometry g, const typename Epi::Out& o_in, hipStream_t st) {
-  if (g.rows == 0) return 0;
-  typename Epi::Out o = o_in;
-  int smax = 1;
-  for (int i = 0; i < g.nseg; ++i) {
-    if (g.seg[i].splits > 16) return fail(STRIDE_TC_EINVAL, "split count above 16");
-    smax = g.seg[i].splits > smax ? g.seg[i].splits : smax;
-  }
-  const int T = g.lane_groups;
-  int kind = 0, idx = 0, rows_per_block = 0;  // kind 0: streaming, 1: pipe, 2: legacy tile, 3: dec
-  const int per = (g.col_tiles >> 1) / smax;
-  const bool forced_stream =
-      g_forced_cfg >= 0 && decode_cfg_fits(kDecodeCfgs[g_forced_cfg], g, smax, Epi::kMats, Epi::kReduce);
-  const bool forced_pipe = g_forced_pipe >= 0 && pipe_cfg_fits(g_forced_pipe, g);
-  const bool forced_dec =
-      g_forced_dec >= 0 && dec_cfg_fits(kDecCfgs[g_forced_dec], g, smax, Epi::kMats, Epi::kReduce);
-  if (forced_dec) {
-    kind = 3;
-    idx = g_forced_dec;
-  } else if (forced_stream) {
-    idx = g_forced_cfg;
-  } else if (forced_pipe) {
-    kind = 1;
-    idx = g_forced_pipe;
-  } else {
-    const Pick p = T <= kStreamMaxLaneTiles ? pick_small(T, smax, Epi::kMats, g.nseg, per) : pick_large(g, T, smax, per);
-    kind = p.kind;
-    idx = p.idx;
-    if (kind == 1 && !pipe_cfg_fits(idx, g)) {
-      idx = pick_pipe(g, smax);
-      if (!pipe_cfg_fits(idx, g)) idx = 0;
-      if (!pipe_cfg_fits(idx, g)) kind = 2;
-    }
-    if (kind == 3 && !dec_cfg_fits(kDecCfgs[idx], g, smax, Epi::kMats, Epi::kReduce)) {
-      kind = 0;
-      idx = pick_decode(T, smax, Epi::kMats, g.nseg, per);
-    }
-    if (kind == 0 && !decode_cfg_fits(kDecodeCfgs[idx], g, smax, Epi::kMats, Epi::kReduce)) {
-      // a register-only in-workgroup configuration with a wave per split always fits
-      idx = smax == 1 ? 3 : (smax == 2 ? 2 : (smax <= 8 ? 0 : 18));
-    }
-  }
-  if (kind == 0) rows_per_block = kDecodeCfgs[idx].wr * kDecodeCfgs[idx].r;
-  if (kind == 1) rows_per_block = pipe_rows_per_block(idx, Epi::kMats);
-  if (kind == 3) rows_per_block = kDecCfgs[idx].nw / kDecCfgs[idx].ws * kDecCfgs[idx].r;
-  // Greedy LM head: two passes through the candidate scratch when it fits.
-  int nrb = 0;
-  if constexpr (Epi::kReduce) {
-    o.cand = nullptr;
-    if (kind != 2 && g.nseg == 1) {
-      nrb = (g.seg[0].row_tiles + rows_per_block - 1) / rows_per_block;
-      if (static_cast<int64_t>(nrb) * g.rows <= kCandSlots) o.cand = scratch_base();
-      if (!o.cand) nrb = 0;
-      o.nrb = nrb;
-    }
-  }
-  if (kind == 0) {
-    g_last_cfg = idx;
-    const bool xs = kDecodeCfgs[idx].xs;
-    if (xs) {
-      g.part = reinterpret_cast<float*>(scratch_base());
-      g.split_cnt = split_counters();
-      g.part_splits = smax;
-      if (!g.part || !g.split_cnt) return fail(STRIDE_TC_EINVAL, "split scratch unavailable");
-    }
-    launch_decode_cfg<Epi>(idx, g, o, st);
-  } else if (kind == 3) {
-    g_last_cfg = kDecIndexBase + idx;
-    if (kDecCfgs[idx].xs) {
-      g.part = reinterpret_cast<float*>(scratch_base());
-      g.split_cnt = split_counters();
-      g.part_splits = smax;
-      if (!g.part || !g.split_cnt) return fail(STRIDE_TC_EINVAL, "split scratch unavailable");
-    }
-    launch_dec_cfg<Epi>(idx, g, o, st);
-  } else if (kind == 1) {
-    g_last_cfg = -3 - idx;
-    launch_pipe_cfg<Epi>(idx, g, o, smax, st);
-  } else {
-    g_last_cfg = -2;
-    if constexpr (Epi::kMats == 2) launch_tile<Epi, 2, 4>(g, o, st);
-    else launch_tile<Epi, 4, 4>(g, o, st);
-  }
-  if constexpr (Epi::kReduce) {
-    if (nrb > 0) hipLaunchKernelGGL(k_argmax_finish, dim3(g.rows), dim3(256), 0, st, o.cand, nrb, g.rows, o.best);
-  }
-  const hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return fail(static_cast<int>(e), std::string("kernel launch failed: ") + hipGetErrorString(e));
-  return 0;
-}
+int g_last_cfg = -1;
 
 // fp32 activations rows [rows][cols] -> two bf16 lane-tile sets, hi = bf16(x) and
 // lo = bf16(x - hi), both round to nearest even; lanes past `rows` are zero.
@@ -684,20 +113,6 @@ __global__ __launch_bounds__(256) void k_zero_f32(float* y, int64_t n) {
   const int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 4;
   if (i + 3 < n) *reinterpret_cast<f32x4*>(y + i) = f32x4{0.f, 0.f, 0.f, 0.f};
   else for (int64_t k = i; k < n; ++k) y[k] = 0.f;
-}
-
-Geometry single(const StrideLanes& l, const uint16_t* x, const StrideGemmMat& m, const uint16_t* w2) {
-  Geometry g{};
-  g.x = x;
-  g.col_tiles = m.cols / 16;
-  g.rows = l.rows;
-  g.lane_groups = l.lane_groups;
-  g.nseg = 1;
-  g.seg[0].w[0] = m.w;
-  g.seg[0].w[1] = w2;
-  g.seg[0].row_tiles = m.groups;
-  g.seg[0].splits = split_count(m.groups * 16, m.cols);
-  return g;
 }
 
 }  // namespace stride_tc
@@ -794,83 +209,6 @@ int stride_tc_gemm_f32x(const StrideTcGemmF32xParams* p, void* stream) {
   EpiResidual::Out o{p->y, p->m.groups};
   if (int rc = run<EpiResidual>(single(p->l, hi, p->m, nullptr), o, st)) return rc;
   return run<EpiResidual>(single(p->l, lo, p->m, nullptr), o, st);
-}
-
-int stride_tc_mlp13(const StrideTcMlp13Params* p, int, int, void* stream) {
-  std::string why;
-  if (!p) return fail(STRIDE_TC_EINVAL, "mlp13: null params");
-  if (!lanes_ok(p->l, why) || !mat_ok(p->w1, "mlp13.w1", why) || !mat_ok(p->w3, "mlp13.w3", why))
-    return fail(STRIDE_TC_EINVAL, "mlp13: " + why);
-  if (p->w1.groups != p->w3.groups || p->w1.cols != p->w3.cols) return fail(STRIDE_TC_EINVAL, "mlp13: w1 and w3 shapes differ");
-  if (!p->x || !p->z) return fail(STRIDE_TC_EINVAL, "mlp13: null x or z");
-  Geometry g = single(p->l, p->x, p->w1, p->w3.w);
-  EpiGateUp::Out o{p->z, p->w1.groups};
-  return run<EpiGateUp>(g, o, static_cast<hipStream_t>(stream));
-}
-
-int stride_tc_lm_full(const StrideTcLmFullParams* p, int, void* stream) {
-  std::string why;
-  if (!p) return fail(STRIDE_TC_EINVAL, "lm_full: null params");
-  if (!lanes_ok(p->l, why) || !mat_ok(p->m, "lm_full.m", why)) return fail(STRIDE_TC_EINVAL, "lm_full: " + why);
-  if (!p->x || !p->logits) return fail(STRIDE_TC_EINVAL, "lm_full: null x or logits");
-  Geometry g = single(p->l, p->x, p->m, nullptr);
-  EpiLogits::Out o{p->logits};
-  return run<EpiLogits>(g, o, static_cast<hipStream_t>(stream));
-}
-
-int stride_tc_lm_greedy(const StrideTcLmGreedyParams* p, int, int, void* stream) {
-  std::string why;
-  if (!p) return fail(STRIDE_TC_EINVAL, "lm_greedy: null params");
-  if (!lanes_ok(p->l, why) || !mat_ok(p->m, "lm_greedy.m", why)) return fail(STRIDE_TC_EINVAL, "lm_greedy: " + why);
-  if (!p->x || !p->best) return fail(STRIDE_TC_EINVAL, "lm_greedy: null x or best");
-  if (p->vocab <= 0 || p->vocab > p->m.groups * 16) return fail(STRIDE_TC_EINVAL, "lm_greedy: vocab must be in (0, groups*16]");
-  Geometry g = single(p->l, p->x, p->m, nullptr);
-  EpiArgmax::Out o{p->best, p->vocab, nullptr, 0};
-  return run<EpiArgmax>(g, o, static_cast<hipStream_t>(stream));
-}
-
-int stride_tc_qkv(const StrideTcQkvParams* p, void* stream) {
-  std::string why;
-  if (!p) return fail(STRIDE_TC_EINVAL, "qkv: null params");
-  if (!lanes_ok(p->l, why) || !mat_ok(p->q, "qkv.q", why) || !mat_ok(p->k, "qkv.k", why) || !mat_ok(p->v, "qkv.v", why))
-    return fail(STRIDE_TC_EINVAL, "qkv: " + why);
-  if (p->q.cols != p->k.cols || p->q.cols != p->v.cols || p->k.groups != p->v.groups)
-    return fail(STRIDE_TC_EINVAL, "qkv: q, k, v must share cols and k, v must have equal groups");
-  const int D = p->head_dim;
-  if (D <= 0 || D % 16 != 0 || (p->q.groups * 16) % D != 0 || (p->k.groups * 16) % D != 0)
-    return fail(STRIDE_TC_EINVAL, "qkv: head_dim must be a multiple of 16 dividing the q and k rows");
-  if (!p->x || !p->q_out || !p->rope || !p->row_slot || !p->row_pos || !p->kv.arena || !p->kv.table)
-    return fail(STRIDE_TC_EINVAL, "qkv: null pointer argument");
-  if (p->kv.head_dim != D || p->kv.group_elems <= 0 || p->kv.group_elems % D != 0)
-    return fail(STRIDE_TC_EINVAL, "qkv: kv.head_dim must equal head_dim and kv.group_elems must be tokens*head_dim");
-  const int64_t page = p->kv.group_elems / D;
-  int shift = 0;
-  while ((int64_t{1} << shift) < page) ++shift;
-  if ((int64_t{1} << shift) != page) return fail(STRIDE_TC_EINVAL, "qkv: KV page size (group_elems/head_dim) must be a power of two");
-  Geometry g{};
-  g.x = p->x;
-  g.col_tiles = p->q.cols / 16;
-  g.rows = p->l.rows;
-  g.lane_groups = p->l.lane_groups;
-  g.nseg = 3;
-  const StrideGemmMat* mats[3] = {&p->q, &p->k, &p->v};
-  for (int i = 0; i < 3; ++i) {
-    g.seg[i].w[0] = mats[i]->w;
-    g.seg[i].w[1] = nullptr;
-    g.seg[i].row_tiles = mats[i]->groups;
-    g.seg[i].splits = split_count(mats[i]->groups * 16, mats[i]->cols);
-  }
-  EpiQkv::Out o{};
-  o.q_out = p->q_out;
-  o.q_stride = p->q_stride;
-  o.layer = p->layer;
-  o.head_dim = D;
-  o.page_shift = shift;
-  o.kv = p->kv;
-  o.rope = p->rope;
-  o.row_slot = p->row_slot;
-  o.row_pos = p->row_pos;
-  return run<EpiQkv>(g, o, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"
