@@ -471,6 +471,7 @@ inline Pick pick_small(int T, int smax, int mats, int nseg, int per) {
   if (smax == 1 && T >= 2) return {1, T <= 4 ? 14 : 8};
   if (smax == 2 && mats == 2 && T >= 3 && T <= 4) return {3, 13};
   if (smax == 2 && mats == 2 && T >= 3) return {1, 15};
+  if (smax == 8 && nseg == 1 && per >= 32 && T == 4) return {3, 7};  // long splits (down), one split per workgroup
   return {0, pick_decode(T, smax, mats, nseg, per)};
 }
 

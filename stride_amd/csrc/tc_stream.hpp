@@ -23,6 +23,12 @@ namespace stride_tc {
 // Largest split count served by cross-workgroup split launches (XS).
 constexpr int kMaxXSplits = 8;
 
+// Buffer-instruction cache policy bit sc1 (device-scope coherence on gfx950) and
+// word 3 of a raw, untyped buffer resource.
+constexpr int kCachePolicySc1 = 16;
+constexpr int kRawBufferWord3 = 0x00020000;
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+
 // Output-tile and unit bases of segment si for the cross-workgroup split scratch.
 __device__ __forceinline__ int xs_tile0(const Geometry& g, int si) {
   int t = 0;
@@ -67,9 +73,14 @@ __device__ __forceinline__ void xs_finish(const Geometry& g, const typename Epi:
     return;
   }
   const int tile0 = xs_tile0(g, si);
-  auto slot = [&](int r, int l, int s, int m) {
-    const int64_t tile = tile0 + static_cast<int64_t>(rt_first + r) * g.lane_groups + lt0 + l;
-    return reinterpret_cast<uint64_t*>(g.part) + ((tile * g.part_splits + s) * M + m) * (2 * kWave) + 2 * lane;
+  // Partial tiles travel as 16-byte buffer stores and loads with the sc1 cache
+  // policy, which makes them coherent at device scope across XCDs (the policy
+  // the compiler gives agent-scope relaxed atomics on this target), four lanes
+  // to a full 64-byte segment. Byte offsets stay below the 16 MiB scratch.
+  const __amdgpu_buffer_rsrc_t part = __builtin_amdgcn_make_buffer_rsrc(g.part, 0, 0x7fffffff, kRawBufferWord3);
+  auto offset = [&](int r, int l, int s, int m) -> int {
+    const int tile = tile0 + (rt_first + r) * g.lane_groups + lt0 + l;
+    return (((tile * g.part_splits + s) * M + m) * kWave + lane) * 16;
   };
 #pragma unroll
   for (int r = 0; r < R; ++r) {
@@ -78,14 +89,9 @@ __device__ __forceinline__ void xs_finish(const Geometry& g, const typename Epi:
     for (int l = 0; l < LT; ++l) {
       if (l >= nlt) continue;
 #pragma unroll
-      for (int m = 0; m < M; ++m) {
-        uint64_t* p = slot(r, l, my_split, m);
-        const f32x4 v = acc[m][r][l];
-        __hip_atomic_store(p, static_cast<uint64_t>(u32_of(v[0])) | (static_cast<uint64_t>(u32_of(v[1])) << 32),
-                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(p + 1, static_cast<uint64_t>(u32_of(v[2])) | (static_cast<uint64_t>(u32_of(v[3])) << 32),
-                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
+      for (int m = 0; m < M; ++m)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, acc[m][r][l]), part, offset(r, l, my_split, m), 0,
+                                               kCachePolicySc1);
     }
   }
   // The partial stores are complete (performed at device scope) before this
@@ -108,18 +114,13 @@ __device__ __forceinline__ void xs_finish(const Geometry& g, const typename Epi:
       if (l >= nlt) continue;
       // Issue every partial load first (at most kMaxXSplits splits, a
       // wave-uniform bound), then fold in ascending split order.
-      f32x4 part[kMaxXSplits][M];
+      f32x4 pv[kMaxXSplits][M];
 #pragma unroll
       for (int s = 0; s < kMaxXSplits; ++s) {
         if (s >= splits || s == my_split) continue;
 #pragma unroll
-        for (int m = 0; m < M; ++m) {
-          const uint64_t* p = slot(r, l, s, m);
-          const uint64_t lo = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          const uint64_t hi = __hip_atomic_load(p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          part[s][m] = f32x4{f32_of(static_cast<uint32_t>(lo)), f32_of(static_cast<uint32_t>(lo >> 32)),
-                             f32_of(static_cast<uint32_t>(hi)), f32_of(static_cast<uint32_t>(hi >> 32))};
-        }
+        for (int m = 0; m < M; ++m)
+          pv[s][m] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(part, offset(r, l, s, m), 0, kCachePolicySc1));
       }
       f32x4 y[M];
 #pragma unroll
@@ -127,7 +128,7 @@ __device__ __forceinline__ void xs_finish(const Geometry& g, const typename Epi:
         if (s >= splits) continue;
 #pragma unroll
         for (int m = 0; m < M; ++m) {
-          const f32x4 v = s == my_split ? acc[m][r][l] : part[s][m];
+          const f32x4 v = s == my_split ? acc[m][r][l] : pv[s][m];
           y[m] = s == 0 ? v : y[m] + v;
         }
       }
