@@ -168,23 +168,27 @@ def capture(torch, fns, reps=1):
     return g
 
 
-def time_ops(torch, ops, reps):
-    """Average device time per launch of each op name: a HIP graph of `reps`
-    passes over that op's launches (one per layer, so weights rotate), replayed
-    twice between HIP events recorded on the replay stream."""
+def time_ops(torch, ops, reps, replays=5):
+    """Device time per launch of each op name: a HIP graph of `reps` passes over
+    that op's launches (one per layer, so weights rotate), replayed `replays`
+    times, each replay between HIP events recorded on the replay stream. Returns
+    {name: (median, min, max)} seconds per launch over the replays."""
     names = sorted({n for n, _ in ops})
     res = {}
     for name in names:
         sel = [f for n, f in ops if n == name]
         g = capture(torch, sel, reps)
         stream = torch.cuda.current_stream()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        g.replay()
-        g.replay()
-        e1.record(stream)
-        e1.synchronize()
-        res[name] = e0.elapsed_time(e1) / 1e3 / (2 * reps * len(sel))
+        per = []
+        for _ in range(replays):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            g.replay()
+            e1.record(stream)
+            e1.synchronize()
+            per.append(e0.elapsed_time(e1) / 1e3 / (reps * len(sel)))
+        per.sort()
+        res[name] = (per[len(per) // 2], per[0], per[-1])
         del g
     return res
 
@@ -249,11 +253,33 @@ def cpu_baseline(seconds, threads):
             ex.gemm(w, x)
             t[name] = time.perf_counter() - t0
     step = LAYERS * (t["qkv"] + t["o"] + t["gate_up"] + t["down"]) + t["lm_head"]
+    flops = {name: 2 * n * k for name, n, k, _ in shapes}
+    nbytes = {name: 2 * n * k + 4 * k + 4 * n for name, n, k, _ in shapes}  # bf16 W, fp32 x and y
     return {"value": round(1.0 / step, 3), "unit": "tok/s", "cores": threads, "kind": kind,
             "sample": "batch-1 decode step, exact path: one layer's QKV/O/gate+up/down GEMMs + LM head timed "
                       "(k_lm_full order, all fmaf chains), layer time x16 + LM head; STRIDE_CPU_THREADS="
                       f"{threads}", "seconds_per_step": round(step, 4),
-            "per_gemm_ms": {k: round(v * 1e3, 3) for k, v in t.items()}}
+            "per_gemm_ms": {k: round(v * 1e3, 3) for k, v in t.items()},
+            "per_gemm_GB/s": {k: round(nbytes[k] / v / 1e9, 2) for k, v in t.items()},
+            "per_gemm_GFLOP/s": {k: round(flops[k] / v / 1e9, 2) for k, v in t.items()}}
+
+
+def cpu_baseline_single_core(seconds):
+    """The same sample on one core. The reference's thread pool reads its size
+    once per process, so this runs in a child process with STRIDE_CPU_THREADS=1."""
+    import subprocess
+
+    env = dict(os.environ, STRIDE_CPU_THREADS="1")
+    code = f"import json, bench; print(json.dumps(bench.cpu_baseline({seconds!r}, 1)))"
+    try:
+        r = subprocess.run([sys.executable, "-c", code], cwd=ROOT, env=env, capture_output=True, text=True,
+                           timeout=120 + 4 * seconds)
+    except subprocess.TimeoutExpired:
+        return None
+    if r.returncode != 0 or not r.stdout.strip():
+        return None
+    one = json.loads(r.stdout.strip().splitlines()[-1])
+    return {k: one[k] for k in ("value", "unit", "cores", "seconds_per_step", "per_gemm_ms", "per_gemm_GB/s")}
 
 
 def engine_step(torch, dev, m, steps, warmup, position=383):
@@ -337,10 +363,10 @@ def main():
         if not sel:
             print(f"bench.py: unknown --op {a.op}", file=sys.stderr)
             sys.exit(2)
-        sec = time_ops(torch, sel, max(1, a.steps // len(sel)))[a.op]
+        sec, lo, hi = time_ops(torch, sel, max(1, a.steps // len(sel)))[a.op]
         f, byt = work(a.op, a.m)
-        print(json.dumps({"op": a.op, "M": a.m, "us": round(sec * 1e6, 2), "GB/s": round(byt / sec / 1e9, 1),
-                          "TFLOP/s": round(f / sec / 1e12, 1)}), flush=True)
+        print(json.dumps({"op": a.op, "M": a.m, "us": round(sec * 1e6, 2), "spread_us": [round(lo * 1e6, 2), round(hi * 1e6, 2)],
+                          "GB/s": round(byt / sec / 1e9, 1), "TFLOP/s": round(f / sec / 1e12, 1)}), flush=True)
         return
 
     if a.copy_calib_mib:
@@ -381,15 +407,19 @@ def main():
     value = a.m * a.steps / dt
     del graph
 
-    # Per-kernel averages at the bench M (dominant kernel -> roofline object).
-    per = time_ops(torch, ops, 3)
+    # Per-kernel times at the bench M (dominant kernel -> roofline object): the
+    # median over graph replays, with the fastest and slowest replay beside it.
+    spread = time_ops(torch, ops, 3)
+    per = {n: v[0] for n, v in spread.items()}
     share = {n: per[n] * sum(1 for o, _ in ops if o == n) for n in per}
     dom = max(share, key=share.get)
     fl, by = work(dom, a.m)
     ach = by / per[dom] / 1e9
     roof = {"kernel": dom, "bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dom, a.m),
-            "avg_launch_us": round(per[dom] * 1e6, 2), "algorithmic_bytes": int(by)}
+            "avg_launch_us": round(per[dom] * 1e6, 2),
+            "launch_us_spread": [round(spread[dom][1] * 1e6, 2), round(spread[dom][2] * 1e6, 2)],
+            "algorithmic_bytes": int(by)}
     weight_bytes = sum(work(n, 0)[1] for n, _ in ops)
 
     table = []
@@ -398,13 +428,13 @@ def main():
             bm = b if m == a.m else Buffers(torch, dev, m)
             t = time_ops(torch, step_ops(model, bm), 2 if m >= 1024 else 3)
             row = {"M": m}
-            for n, sec in sorted(t.items()):
+            for n, (sec, lo, hi) in sorted(t.items()):
                 f, byt = work(n, m)
                 gbs, tfl = byt / sec / 1e9, f / sec / 1e12
                 bound = "hbm" if m <= 128 else "mfma"
                 frac = gbs / HBM_PEAK_GBS if bound == "hbm" else tfl / MFMA_BF16_PEAK_TFLOPS
-                row[n] = {"us": round(sec * 1e6, 2), "GB/s": round(gbs, 1), "TFLOP/s": round(tfl, 2),
-                          "frac": round(frac, 4), "bound": bound}
+                row[n] = {"us": round(sec * 1e6, 2), "spread_us": [round(lo * 1e6, 2), round(hi * 1e6, 2)],
+                          "GB/s": round(gbs, 1), "TFLOP/s": round(tfl, 2), "frac": round(frac, 4), "bound": bound}
             table.append(row)
             del bm
             torch.cuda.empty_cache()
@@ -412,6 +442,8 @@ def main():
     full = engine_step(torch, dev, a.m, a.steps, a.warmup) if a.engine else None
     library = library_gemm(torch, dev) if a.library else None
     cpu = cpu_baseline(a.cpu_seconds, a.cpu_threads) if a.cpu_seconds > 0 else None
+    if cpu is not None and a.cpu_threads != 1:
+        cpu["single_core"] = cpu_baseline_single_core(a.cpu_seconds / 2)
     out = {
         "metric": "Llama-3.2-1B GEMM GB/s & TFLOP/s (% roofline) at M=1..4096; decode tok/s",
         "value": round(value, 1), "unit": "tok/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
