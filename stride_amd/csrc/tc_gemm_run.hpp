@@ -389,9 +389,13 @@ void launch_pipe(Geometry g, const typename Epi::Out& o, int smax, hipStream_t s
   X(24, 8, 8, 2, 2, 1, 4, 1, 0) \
   X(25, 4, 8, 2, 2, 1, 6, 1, 0) \
   X(26, 4, 4, 4, 2, 2, 3, 1, 1) \
-  X(27, 4, 4, 2, 4, 1, 5, 1, 1)
+  X(27, 4, 4, 2, 4, 1, 5, 1, 1) \
+  X(28, 4, 4, 2, 4, 2, 3, 1, 0) \
+  X(29, 4, 4, 2, 4, 1, 4, 1, 0) \
+  X(30, 4, 4, 2, 4, 1, 6, 1, 0) \
+  X(31, 4, 8, 2, 2, 1, 4, 1, 0)
 
-constexpr int kNumPipeCfgs = 28;
+constexpr int kNumPipeCfgs = 32;
 extern int g_forced_pipe;
 
 template <class Epi>
@@ -480,18 +484,20 @@ inline Pick pick_small(int T, int smax, int mats, int nseg, int per) {
 // whose waves run the splits side by side, beats the pipeline, which walks them
 // one after another; beyond, the pipeline with a block shape per size.
 inline Pick pick_large(const Geometry& g, int T, int smax, int per) {
-  if (smax == 1) return {1, T <= 12 || T > 24 ? 3 : 8};
+  if (smax == 1) return {1, T <= 12 ? 3 : (T <= 24 ? 8 : 6)};
   if (smax == 2) {
     if (T <= 12) return {1, 12};
     if (T <= 24) return {1, 8};
     if (T <= 48) return {1, 2};
-    return {1, pick_pipe(g, smax)};
+    if (T <= 64) return {1, pick_pipe(g, smax)};
+    return {1, 28};
   }
   if (g.nseg == 3) {  // fused QKV
     if (T <= 12) return {0, 33};
     if (T <= 24) return {0, 29};
-    if (T <= 64) return {1, 12};
-    return {1, 2};
+    if (T <= 64) return {1, 14};
+    if (T <= 128) return {1, 28};
+    return {1, 26};
   }
   if (per >= 32) {  // long splits (down)
     if (T <= 12) return {0, 27};
