@@ -500,6 +500,7 @@ inline Pick pick_large(const Geometry& g, int T, int smax, int per) {
     return {1, 26};
   }
   if (per >= 32) {  // long splits (down)
+    if (T <= 12 && dec_cfg_fits(kDecCfgs[7], g, smax, 1, false)) return {3, 7};  // one split per workgroup
     if (T <= 12) return {0, 27};
     if (T <= 32) return {0, 29};
     if (T <= 64) return {0, 30};
