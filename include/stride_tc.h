@@ -28,6 +28,13 @@
  * value, or STRIDE_TC_EINVAL for rejected arguments); stride_tc_last_error()
  * describes the last failure on the calling thread. Launches are asynchronous on
  * `stream` (NULL = the default stream); nothing here synchronizes or allocates.
+ *
+ * Shared device state: GEMM launches that combine splits across workgroups, and
+ * the greedy LM head, use one 16 MiB device-global scratch array and a set of
+ * arrival counters per device. Launches on one device must therefore be ordered
+ * (one stream, as the reference keeps them, src/kernels.cu:457-460); launches
+ * that overlap on one device race. The configuration hooks below are
+ * process-wide and meant for tuning sweeps, not for concurrent callers.
  */
 #ifndef STRIDE_TC_H
 #define STRIDE_TC_H
