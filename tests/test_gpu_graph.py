@@ -1,0 +1,93 @@
+"""Captured HIP graphs replay to the same bits as eager launches. The benchmark and
+the engine both run the GEMMs from a graph; the cross-workgroup split combine
+(arrival counters re-armed by the last workgroup, no memset node) and the greedy
+LM head's candidate scratch must give the eager result on every replay, with other
+eager work between replays. Each replay first restores its inputs with copy
+kernels captured in the same graph."""
+import hashlib
+
+import pytest
+import torch
+
+from stride_amd import _lib, harness, layout
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+def digest(t):
+    return hashlib.sha256(t.cpu().numpy().tobytes()).hexdigest()
+
+
+@pytest.fixture(scope="module")
+def data():
+    g = torch.Generator(device=DEV).manual_seed(91)
+
+    def w(n, k):
+        return layout.pack_tiles((torch.randn(n, k, generator=g, device=DEV) * 0.02).to(torch.bfloat16).view(torch.int16))
+
+    W = dict(o=w(2048, 2048), down=w(512, 8192), w1=w(1024, 2048), w3=w(1024, 2048), lm=w(4000, 2048))
+    rows = max(m for m, _ in CASES)
+    x = {k: (torch.randn(rows, k, generator=g, device=DEV)).to(torch.bfloat16).view(torch.int16) for k in (2048, 8192)}
+    h = torch.randn(rows, 2048, generator=g, device=DEV)
+    return W, x, h
+
+
+def launch_set(W, xt, xd, h_o0, h_d0, h_o, h_d, best, best0, z, m):
+    h_o.copy_(h_o0)
+    h_d.copy_(h_d0)
+    best.copy_(best0)
+    harness.gemm_residual(W["o"], xt, h_o, m)
+    harness.gemm_residual(W["down"], xd, h_d, m)
+    harness.mlp13(W["w1"], W["w3"], xt, m, out=z)
+    harness.lm_greedy(W["lm"], xt, m, 3990, best=best)
+
+
+# (M, forced configuration): the automatic choice, cross-workgroup split configurations
+# of the streaming kernel (53) and of k_dec (1007), and the pipeline.
+CASES = [(1, -1), (1, 53), (64, -1), (64, 1007), (128, -1), (290, -1)]
+
+
+@pytest.mark.parametrize("m,cfg", CASES)
+def test_graph_replays_match_eager(data, m, cfg):
+    W, x, h = data
+    say("graph replay M =", m, "config", cfg)
+    assert x[2048].shape[0] >= m and h.shape[0] >= m, "activations must hold M rows"  # the kernels read M rows
+    xt = layout.lane_tiles(x[2048][:m])
+    xd = layout.lane_tiles(x[8192][:m])
+    h_o0 = layout.lane_tiles(h[:m].clone())
+    h_d0 = layout.lane_tiles(h[:m, :512].clone())
+    h_o, h_d = torch.empty_like(h_o0), torch.empty_like(h_d0)
+    best0 = harness.best_init(m, DEV)
+    best = torch.empty_like(best0)
+    z = torch.zeros(((m + 15) // 16, W["w1"].shape[0], 16, 16), dtype=torch.int16, device=DEV)
+    _lib.set_stream_config(cfg)
+    try:
+        launch_set(W, xt, xd, h_o0, h_d0, h_o, h_d, best, best0, z, m)
+        torch.cuda.synchronize()
+        ref = [digest(t) for t in (h_o, h_d, z, best)]
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            launch_set(W, xt, xd, h_o0, h_d0, h_o, h_d, best, best0, z, m)  # warm-up on the capture stream
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            launch_set(W, xt, xd, h_o0, h_d0, h_o, h_d, best, best0, z, m)
+        scratch_h = layout.lane_tiles(h[:m].clone())
+        for rep in range(4):
+            for t in (h_o, h_d, z, best):
+                t.fill_(0)  # replays must rebuild every output
+            graph.replay()
+            torch.cuda.synchronize()
+            got = [digest(t) for t in (h_o, h_d, z, best)]
+            assert got == ref, f"replay {rep} differs from eager (M={m}, config {cfg})"
+            harness.gemm_residual(W["o"], xt, scratch_h, m)  # eager work between replays
+            torch.cuda.synchronize()
+        del graph
+    finally:
+        _lib.set_stream_config(-1)
