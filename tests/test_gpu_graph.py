@@ -91,3 +91,43 @@ def test_graph_replays_match_eager(data, m, cfg):
         del graph
     finally:
         _lib.set_stream_config(-1)
+
+
+def test_engine_step_graph_replays_match_eager():
+    """One full decode step of the engine (every layer's norm, QKV + KV append,
+    attention, O, gate/up, down, then the greedy LM head) captured as a graph, as
+    the benchmark runs it: each replay returns the eager step's tokens and logit
+    bits (the step rewrites the same KV entries with the same values)."""
+    import numpy as np
+
+    from stride_amd import engine
+
+    cfg = engine.LlamaConfig()
+    say("engine graph: building weights")
+    w = engine.Weights(cfg, DEV, seed=7, max_positions=128)
+    eng = engine.Engine(w, slots=4, max_ctx=96, max_rows=96, page_tokens=16, shuffle_seed=2)
+    rng = np.random.default_rng(1)
+    seqs = [engine.Sequence(i, rng.integers(0, cfg.vocab, 70).tolist()) for i in range(4)]
+    eng.prefill(seqs)
+    rows = [(s.slot, len(s.prompt), s.tokens[-1]) for s in seqs]
+    slot, pos, tok, items = eng.device_rows(rows)
+    best = torch.empty((len(rows), 2), dtype=torch.int32, device=DEV)
+    eng.launch(len(rows), slot, pos, tok, items, best=best)
+    torch.cuda.synchronize()
+    ref = digest(best)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        eng.launch(len(rows), slot, pos, tok, items, best=best)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        eng.launch(len(rows), slot, pos, tok, items, best=best)
+    for rep in range(3):
+        best.fill_(0)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert digest(best) == ref, f"engine step replay {rep} differs from eager"
+        eng.launch(len(rows), slot, pos, tok, items)  # eager work between replays (no LM head)
+        torch.cuda.synchronize()
+    del graph
