@@ -42,7 +42,8 @@ def parse():
     ap.add_argument("--m", type=int, default=128, help="decode batch (activation rows)")
     ap.add_argument("--table", type=int, default=1, help="per-GEMM table over M (0 to skip)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline budget (0 to skip)")
-    ap.add_argument("--cpu-threads", type=int, default=16)
+    ap.add_argument("--cpu-threads", type=int, default=0,
+                    help="threads for the CPU baseline (0: the cores this process may use, at most 16)")
     ap.add_argument("--library", type=int, default=1,
                     help="also time torch.matmul (hipBLASLt) bf16 on the five shapes at M=4096 as context (0 to skip)")
     ap.add_argument("--op", default="", help="time only this GEMM (qkv, o, gate_up, down, lm_head) at --m and print "
@@ -76,7 +77,29 @@ class Model:
                 v=w(KV_HEADS * HEAD_DIM, HIDDEN, layout.rope_rows(KV_HEADS * HEAD_DIM, HEAD_DIM)),
                 o=w(HIDDEN, HEADS * HEAD_DIM), w1=w(FFN, HIDDEN), w3=w(FFN, HIDDEN), w2=w(HIDDEN, FFN)))
         self.lm = w(VOCAB, HIDDEN)
+        self._torch = torch
+        self._rot = {}
         torch.cuda.synchronize()
+
+    def rotation(self, name):
+        """Distinct weight sets for timing `name` alone: the 16 layers, extended
+        with copies (distinct memory) until one pass over them reads at least
+        ROTATION_BYTES, so the 256 MB MALL cannot serve a repeat. The LM head is
+        one matrix; two copies of it are rotated."""
+        if name not in self._rot:
+            keys = OP_WEIGHTS[name]
+            if name == "lm_head":
+                sets = [{"lm": self.lm}, {"lm": self.lm.clone()}]
+            else:
+                sets = [{k: L[k] for k in keys} for L in self.layers]
+                per = sum(sets[0][k].numel() * 2 for k in keys)
+                i = 0
+                while len(sets) * per < ROTATION_BYTES:
+                    sets.append({k: self.layers[i % LAYERS][k].clone() for k in keys})
+                    i += 1
+            self._torch.cuda.synchronize()
+            self._rot[name] = sets
+        return self._rot[name]
 
 
 class Buffers:
@@ -109,21 +132,42 @@ class Buffers:
         self.best0 = harness.best_init(m, dev)
 
 
-def step_ops(model, b):
-    """The launches of one decode step, as (name, callable) pairs."""
+# Weights each op reads, and the least bytes one pass of a per-op timing graph reads.
+OP_WEIGHTS = {"qkv": ("q", "k", "v"), "o": ("o",), "gate_up": ("w1", "w3"), "down": ("w2",), "lm_head": ("lm",)}
+ROTATION_BYTES = 512 << 20
+
+
+def op_launch(name, W, b, li=0):
+    """One launch of op `name` over weight set W (a dict holding OP_WEIGHTS[name])."""
     from stride_amd import harness
 
-    ops = []
     m = b.m
-    for li, L in enumerate(model.layers):
-        ops.append(("qkv", lambda L=L, li=li: harness.qkv(L["q"], L["k"], L["v"], b.x, m, HEAD_DIM, b.rope, b.slots,
-                                                          b.pos, b.kv, layer=li, q_out=b.q)))
-        ops.append(("o", lambda L=L: harness.gemm_residual(L["o"], b.attn, b.h, m)))
-        ops.append(("gate_up", lambda L=L: harness.mlp13(L["w1"], L["w3"], b.x, m, out=b.z)))
-        ops.append(("down", lambda L=L: harness.gemm_residual(L["w2"], b.z, b.h, m)))
+    if name == "qkv":
+        return lambda: harness.qkv(W["q"], W["k"], W["v"], b.x, m, HEAD_DIM, b.rope, b.slots, b.pos, b.kv,
+                                   layer=li % LAYERS, q_out=b.q)
+    if name == "o":
+        return lambda: harness.gemm_residual(W["o"], b.attn, b.h, m)
+    if name == "gate_up":
+        return lambda: harness.mlp13(W["w1"], W["w3"], b.x, m, out=b.z)
+    if name == "down":
+        return lambda: harness.gemm_residual(W["w2"], b.z, b.h, m)
     # best is re-initialised before every argmax, as the engine uploads {-inf, -1}
     # each step (reference src/engine.cpp:423-424); the reset is part of the op.
-    ops.append(("lm_head", lambda: (b.best.copy_(b.best0), harness.lm_greedy(model.lm, b.x, m, VOCAB, best=b.best))))
+    return lambda: (b.best.copy_(b.best0), harness.lm_greedy(W["lm"], b.x, m, VOCAB, best=b.best))
+
+
+def rotated_ops(model, b, names):
+    """(name, launch) pairs for per-op timing: each op over its rotation set."""
+    return [(n, op_launch(n, W, b, li)) for n in names for li, W in enumerate(model.rotation(n))]
+
+
+def step_ops(model, b):
+    """The launches of one decode step, as (name, callable) pairs."""
+    ops = []
+    for li, L in enumerate(model.layers):
+        for n in ("qkv", "o", "gate_up", "down"):
+            ops.append((n, op_launch(n, L, b, li)))
+    ops.append(("lm_head", op_launch("lm_head", {"lm": model.lm}, b)))
     return ops
 
 
@@ -149,6 +193,11 @@ def work(name, m):
     return 2.0 * m * n * k, 2.0 * n * k + 2.0 * m * k + out
 
 
+def rotated_bytes(model, name):
+    """Weight bytes one pass over op `name`'s rotation set reads."""
+    return int(sum(t.numel() * 2 for W in model.rotation(name) for t in W.values()))
+
+
 def capture(torch, fns, reps=1):
     """A HIP graph of `reps` passes over the launches in `fns` (the C-ABI entry
     points launch on torch's current stream, which is the capture stream here)."""
@@ -170,9 +219,10 @@ def capture(torch, fns, reps=1):
 
 def time_ops(torch, ops, reps, replays=5):
     """Device time per launch of each op name: a HIP graph of `reps` passes over
-    that op's launches (one per layer, so weights rotate), replayed `replays`
-    times, each replay between HIP events recorded on the replay stream. Returns
-    {name: (median, min, max)} seconds per launch over the replays."""
+    that op's launches (one per weight set of its rotation, so weights stream from
+    HBM), replayed `replays` times, each replay between HIP events recorded on the
+    replay stream. Returns {name: (median, min, max)} seconds per launch over the
+    replays."""
     names = sorted({n for n, _ in ops})
     res = {}
     for name in names:
@@ -211,10 +261,35 @@ def measured_traffic(op, m):
     return int(hits[0]) if len(hits) == 1 else None
 
 
-def cpu_baseline(seconds, threads):
+def host_info():
+    """Host cores (as os.cpu_count() reports them), the cores this process may run
+    on, and the CPU model string."""
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"host_cores": os.cpu_count(), "affinity_cores": len(os.sched_getaffinity(0)), "cpu_model": model}
+
+
+def cpu_threads_default():
+    """Threads for the CPU baseline: every core this process may use, capped at
+    the 16-core share a one-GPU job is given on the GPU hosts (OMP_NUM_THREADS
+    there holds that share)."""
+    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or 16
+    return max(1, min(len(os.sched_getaffinity(0)), share))
+
+
+def cpu_baseline(seconds, threads, batches=(128, 1)):
     """The reference's exact path (oracle/_ref: its src/kernels.cu compiled as C++)
-    on this host: one decode step at batch 1, sampled as one layer's four GEMMs
-    plus the LM head and scaled to 16 layers."""
+    on this host: one decode step's GEMM set at each batch in `batches`, sampled
+    as one layer's QKV, O, gate+up and down GEMMs plus the LM head (the config-2
+    and config-3 shapes), with the layer time scaled to 16 layers. `value` is the
+    first batch's (the benchmark's M = 128) tok/s."""
     import ctypes as C
 
     import numpy as np
@@ -228,49 +303,59 @@ def cpu_baseline(seconds, threads):
     def wts(n, k):
         return (rng.standard_normal((n, k), dtype=np.float32) * 0.02).view(np.uint32).__rshift__(16).astype(np.uint16)
 
-    x1 = rng.standard_normal((1, HIDDEN), dtype=np.float32)
-    x2 = rng.standard_normal((1, FFN), dtype=np.float32)
-    shapes = [("qkv", 3072, HIDDEN, x1), ("o", HIDDEN, HIDDEN, x1), ("gate_up", 2 * FFN, HIDDEN, x1),
-              ("down", HIDDEN, FFN, x2), ("lm_head", VOCAB, HIDDEN, x1)]
-    t = {}
+    dims = [("qkv", 3072, HIDDEN), ("o", HIDDEN, HIDDEN), ("gate_up", 2 * FFN, HIDDEN), ("down", HIDDEN, FFN),
+            ("lm_head", VOCAB, HIDDEN)]
+    lib = None
     if kind == "reference":
         lib = C.CDLL(orc.REF_PATH)
         lib.ref_bench_gemm.restype = C.c_double
         lib.ref_bench_gemm.argtypes = [np.ctypeslib.ndpointer(np.uint16, flags="C_CONTIGUOUS"), C.c_int, C.c_int,
                                        np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS"), C.c_int, C.c_int]
-        budget = seconds / len(shapes)
-        for name, n, k, x in shapes:
-            w = wts(n, k)
-            one = lib.ref_bench_gemm(w, n, k, x, 1, 1)
-            reps = max(1, min(50, int(budget / max(one, 1e-6))))
-            t[name] = lib.ref_bench_gemm(w, n, k, x, 1, reps) / reps
-            del w
     else:
         ex = orc.Exact(threads=threads)
-        for name, n, k, x in shapes:
-            w = wts(n, k)
-            t0 = time.perf_counter()
-            ex.gemm(w, x)
-            t[name] = time.perf_counter() - t0
-    step = LAYERS * (t["qkv"] + t["o"] + t["gate_up"] + t["down"]) + t["lm_head"]
-    flops = {name: 2 * n * k for name, n, k, _ in shapes}
-    nbytes = {name: 2 * n * k + 4 * k + 4 * n for name, n, k, _ in shapes}  # bf16 W, fp32 x and y
-    return {"value": round(1.0 / step, 3), "unit": "tok/s", "cores": threads, "kind": kind,
-            "sample": "batch-1 decode step, exact path: one layer's QKV/O/gate+up/down GEMMs + LM head timed "
-                      "(k_lm_full order, all fmaf chains), layer time x16 + LM head; STRIDE_CPU_THREADS="
-                      f"{threads}", "seconds_per_step": round(step, 4),
+    res = {}
+    budget = seconds / (len(dims) * len(batches))
+    for name, n, k in dims:
+        w = wts(n, k)
+        for m in batches:
+            x = rng.standard_normal((m, k), dtype=np.float32)
+            if lib is not None:
+                one = lib.ref_bench_gemm(w, n, k, x, m, 1)
+                reps = max(1, min(50, int(budget / max(one, 1e-6))))
+                sec = lib.ref_bench_gemm(w, n, k, x, m, reps) / reps if reps > 1 else one
+            else:
+                t0 = time.perf_counter()
+                ex.gemm(w, x)
+                sec = time.perf_counter() - t0
+            res.setdefault(m, {})[name] = sec
+        del w
+    per_batch = {}
+    for m in batches:
+        t = res[m]
+        step = LAYERS * (t["qkv"] + t["o"] + t["gate_up"] + t["down"]) + t["lm_head"]
+        per_batch[m] = {
+            "tok_s": round(m / step, 3), "seconds_per_step": round(step, 4),
             "per_gemm_ms": {k: round(v * 1e3, 3) for k, v in t.items()},
-            "per_gemm_GB/s": {k: round(nbytes[k] / v / 1e9, 2) for k, v in t.items()},
-            "per_gemm_GFLOP/s": {k: round(flops[k] / v / 1e9, 2) for k, v in t.items()}}
+            "per_gemm_GB/s": {nm: round((2 * n * k + 4 * m * (k + n)) / t[nm] / 1e9, 2) for nm, n, k in dims},
+            "per_gemm_GFLOP/s": {nm: round(2 * m * n * k / t[nm] / 1e9, 2) for nm, n, k in dims}}
+    m0 = batches[0]
+    out = {"value": per_batch[m0]["tok_s"], "unit": "tok/s", "cores": threads, "kind": kind,
+           "sample": f"exact path (k_lm_full order, all fmaf chains) at batch {m0}: one layer's QKV/O/gate+up/down "
+                     "GEMMs + the LM head timed, layer time x16 + LM head; STRIDE_CPU_THREADS="
+                     f"{threads}", "seconds_per_step": per_batch[m0]["seconds_per_step"]}
+    out.update(host_info())
+    out["batches"] = {str(m): v for m, v in per_batch.items()}
+    return out
 
 
 def cpu_baseline_single_core(seconds):
-    """The same sample on one core. The reference's thread pool reads its size
-    once per process, so this runs in a child process with STRIDE_CPU_THREADS=1."""
+    """The same sample on one core at batch 1. The reference's thread pool reads
+    its size once per process, so this runs in a child process with
+    STRIDE_CPU_THREADS=1."""
     import subprocess
 
     env = dict(os.environ, STRIDE_CPU_THREADS="1")
-    code = f"import json, bench; print(json.dumps(bench.cpu_baseline({seconds!r}, 1)))"
+    code = f"import json, bench; print(json.dumps(bench.cpu_baseline({seconds!r}, 1, (1,))))"
     try:
         r = subprocess.run([sys.executable, "-c", code], cwd=ROOT, env=env, capture_output=True, text=True,
                            timeout=120 + 4 * seconds)
@@ -279,7 +364,7 @@ def cpu_baseline_single_core(seconds):
     if r.returncode != 0 or not r.stdout.strip():
         return None
     one = json.loads(r.stdout.strip().splitlines()[-1])
-    return {k: one[k] for k in ("value", "unit", "cores", "seconds_per_step", "per_gemm_ms", "per_gemm_GB/s")}
+    return {k: one[k] for k in ("value", "unit", "cores", "seconds_per_step", "batches")}
 
 
 def engine_step(torch, dev, m, steps, warmup, position=383):
@@ -359,10 +444,10 @@ def main():
     b = Buffers(torch, dev, a.m)
     ops = step_ops(model, b)
     if a.op:
-        sel = [(n, f) for n, f in ops if n == a.op]
-        if not sel:
+        if a.op not in OP_WEIGHTS:
             print(f"bench.py: unknown --op {a.op}", file=sys.stderr)
             sys.exit(2)
+        sel = rotated_ops(model, b, [a.op])
         sec, lo, hi = time_ops(torch, sel, max(1, a.steps // len(sel)))[a.op]
         f, byt = work(a.op, a.m)
         print(json.dumps({"op": a.op, "M": a.m, "us": round(sec * 1e6, 2), "spread_us": [round(lo * 1e6, 2), round(hi * 1e6, 2)],
@@ -409,7 +494,7 @@ def main():
 
     # Per-kernel times at the bench M (dominant kernel -> roofline object): the
     # median over graph replays, with the fastest and slowest replay beside it.
-    spread = time_ops(torch, ops, 3)
+    spread = time_ops(torch, rotated_ops(model, b, list(OP_WEIGHTS)), 3)
     per = {n: v[0] for n, v in spread.items()}
     share = {n: per[n] * sum(1 for o, _ in ops if o == n) for n in per}
     dom = max(share, key=share.get)
@@ -419,14 +504,14 @@ def main():
             "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dom, a.m),
             "avg_launch_us": round(per[dom] * 1e6, 2),
             "launch_us_spread": [round(spread[dom][1] * 1e6, 2), round(spread[dom][2] * 1e6, 2)],
-            "algorithmic_bytes": int(by)}
+            "algorithmic_bytes": int(by), "rotated_bytes": rotated_bytes(model, dom)}
     weight_bytes = sum(work(n, 0)[1] for n, _ in ops)
 
     table = []
     if a.table:
         for m in (1, 8, 32, 64, 128, 290, 1024, 2048, 4096):
             bm = b if m == a.m else Buffers(torch, dev, m)
-            t = time_ops(torch, step_ops(model, bm), 2 if m >= 1024 else 3)
+            t = time_ops(torch, rotated_ops(model, bm, list(OP_WEIGHTS)), 2 if m >= 1024 else 3)
             row = {"M": m}
             for n, (sec, lo, hi) in sorted(t.items()):
                 f, byt = work(n, m)
@@ -434,15 +519,17 @@ def main():
                 bound = "hbm" if m <= 128 else "mfma"
                 frac = gbs / HBM_PEAK_GBS if bound == "hbm" else tfl / MFMA_BF16_PEAK_TFLOPS
                 row[n] = {"us": round(sec * 1e6, 2), "spread_us": [round(lo * 1e6, 2), round(hi * 1e6, 2)],
-                          "GB/s": round(gbs, 1), "TFLOP/s": round(tfl, 2), "frac": round(frac, 4), "bound": bound}
+                          "GB/s": round(gbs, 1), "TFLOP/s": round(tfl, 2), "frac": round(frac, 4), "bound": bound,
+                          "rotated_bytes": rotated_bytes(model, n)}
             table.append(row)
             del bm
             torch.cuda.empty_cache()
 
     full = engine_step(torch, dev, a.m, a.steps, a.warmup) if a.engine else None
     library = library_gemm(torch, dev) if a.library else None
-    cpu = cpu_baseline(a.cpu_seconds, a.cpu_threads) if a.cpu_seconds > 0 else None
-    if cpu is not None and a.cpu_threads != 1:
+    threads = a.cpu_threads or cpu_threads_default()
+    cpu = cpu_baseline(a.cpu_seconds, threads) if a.cpu_seconds > 0 else None
+    if cpu is not None and threads != 1:
         cpu["single_core"] = cpu_baseline_single_core(a.cpu_seconds / 2)
     out = {
         "metric": "Llama-3.2-1B GEMM GB/s & TFLOP/s (% roofline) at M=1..4096; decode tok/s",

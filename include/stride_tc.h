@@ -4,7 +4,7 @@
  * src/kernels_tc.cu:677-710.
  *
  * Structs are byte-compatible with the reference's POD parameter blocks
- * (src/kernels.h:112-135, 213-217 and src/kernels_tc.h:27-77): same field order,
+ * (src/kernels.h:23-46, 79-98, 125-128 and src/kernels_tc.h:10-77): same field order,
  * int32 fields, 8-byte pointers, BestEntry 8-byte aligned. A caller that already
  * fills stride::TcGemmResidualParams can pass its address here unchanged.
  *
@@ -47,14 +47,14 @@ extern "C" {
 
 #define STRIDE_TC_EINVAL 0x5354 /* argument rejected before any launch */
 
-/* src/kernels.h:112-116 */
+/* src/kernels.h:23-27 */
 typedef struct StrideGemmMat {
   const uint16_t* w;
   int32_t groups; /* row tiles (N / 16) */
   int32_t cols;   /* K */
 } StrideGemmMat;
 
-/* src/kernels.h:119-128. The page size in tokens is group_elems / head_dim
+/* src/kernels.h:30-39. The page size in tokens is group_elems / head_dim
  * (64 in the reference's KvCache; any power of two here). */
 typedef struct StrideKvRef {
   void* arena;
@@ -67,7 +67,7 @@ typedef struct StrideKvRef {
   int32_t head_dim;
 } StrideKvRef;
 
-/* src/kernels.h:130-135 (stride and bug are ignored by this library) */
+/* src/kernels.h:41-46 (stride and bug are ignored by this library) */
 typedef struct StrideLanes {
   int32_t rows;
   int32_t lane_groups;
@@ -75,7 +75,7 @@ typedef struct StrideLanes {
   int32_t bug;
 } StrideLanes;
 
-/* src/kernels.h:214-217 */
+/* src/kernels.h:125-128 */
 typedef struct StrideBestEntry {
   float value;
   int32_t index;

@@ -344,4 +344,41 @@ int oracle_tc_attention(const float* q, const uint16_t* k, const uint16_t* v, in
   return 0;
 }
 
+// RoPE table (src/model.cpp:54-88; model.cpp itself needs nlohmann/json, which
+// this image lacks, so it is restated here): base = fp32(pow(theta, double(fp32(2i)
+// / fp32(dim)))), f = 1 / base in fp32, llama3 band scaling on the wavelength
+// 2*pi/f in fp32; entry (pos, i) = (fp32(cos(double(fp32(f_i * fp32(pos))))),
+// fp32(sin(...))) with the C library's double cos/sin. table is
+// [max_positions][dim/2][2].
+int oracle_rope_table(int dim, double theta, int llama3, double factor, double low, double high, double orig_ctx,
+                      int max_positions, float* table) {
+  if (dim <= 0 || dim % 2 != 0 || max_positions <= 0) return 1;
+  const int half = dim / 2;
+  std::vector<float> inv(half);
+  const float pi2 = static_cast<float>(2.0 * M_PI);
+  for (int i = 0; i < half; ++i) {
+    const float e = static_cast<float>(2 * i) / static_cast<float>(dim);
+    float f = 1.0f / static_cast<float>(std::pow(theta, static_cast<double>(e)));
+    if (llama3) {
+      const float fac = static_cast<float>(factor);
+      const float low_wave = static_cast<float>(orig_ctx / low);
+      const float high_wave = static_cast<float>(orig_ctx / high);
+      const float wave = pi2 / f;
+      const float smooth = (static_cast<float>(orig_ctx) / wave - static_cast<float>(low)) / static_cast<float>(high - low);
+      if (wave > low_wave)
+        f = f / fac;
+      else if (!(wave < high_wave))
+        f = (1.0f - smooth) * (f / fac) + smooth * f;
+    }
+    inv[i] = f;
+  }
+  for (int pos = 0; pos < max_positions; ++pos)
+    for (int i = 0; i < half; ++i) {
+      const double a = static_cast<double>(inv[i] * static_cast<float>(pos));
+      table[(static_cast<int64_t>(pos) * half + i) * 2] = static_cast<float>(std::cos(a));
+      table[(static_cast<int64_t>(pos) * half + i) * 2 + 1] = static_cast<float>(std::sin(a));
+    }
+  return 0;
+}
+
 }  // extern "C"

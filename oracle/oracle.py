@@ -163,6 +163,17 @@ class Exact(_Base):
             raise ValueError("oracle_tc_norm rejected its arguments")
         return x
 
+    def rope_table(self, cfg, max_positions: int):
+        """RoPE table [max_positions][head_dim/2][2] of a stride_amd.weights.ModelConfig."""
+        half = cfg.head_dim // 2
+        out = np.zeros((max_positions, half, 2), np.float32)
+        f = self.lib.oracle_rope_table
+        f.argtypes = [C.c_int, C.c_double, C.c_int, C.c_double, C.c_double, C.c_double, C.c_double, C.c_int, _f32p]
+        if f(cfg.head_dim, cfg.rope_theta, int(cfg.rope_llama3), cfg.rope_factor, cfg.rope_low, cfg.rope_high,
+             cfg.rope_orig_ctx, max_positions, out) != 0:
+            raise ValueError("oracle_rope_table rejected its arguments")
+        return out
+
     def tc_attention(self, q, k, v, row_slot, row_pos, scale: float):
         """Tensor-core-path attention. q [m][n_kv*4][hd] fp32; k, v [slots][n_kv][cap][hd]
         bf16 bits -> out bf16 bits [m][n_kv*4*hd]."""

@@ -9,7 +9,7 @@
 //   activations dim-major A[dim*stride+lane] (src/kernels.h:3-8, lane_shape
 //                                             src/engine.cpp:24-28)
 // and calls k_lm_full / k_gemm_residual / k_mlp13 / k_lm_greedy / k_qkv, and
-// k_embed / k_norm / k_attention for the non-GEMM operators (src/kernels.h:236-244). Signatures mirror oracle/exact.cpp so the two can be
+// k_embed / k_norm / k_attention for the non-GEMM operators (src/kernels.h:146-155). Signatures mirror oracle/exact.cpp so the two can be
 // compared element for element.
 #include <cstdint>
 #include <cstring>

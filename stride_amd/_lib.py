@@ -1,7 +1,7 @@
 """ctypes binding of libstride_tc.so (the C ABI declared in include/stride_tc.h).
 
 The Structure classes mirror the reference's POD parameter blocks byte for byte
-(src/kernels.h:112-135, 213-217; src/kernels_tc.h:27-77); ``check_layout`` asserts
+(src/kernels.h:23-46, 79-98, 125-128; src/kernels_tc.h:10-77); ``check_layout`` asserts
 the sizes the C++ side static_asserts. Loading fails loudly: there is no fallback
 path, so a missing or stale library is an error, never a silent CPU substitute.
 """

@@ -83,6 +83,10 @@ class Engine:
         dev = self.dev = weights.embed.device
         if cfg.head_dim not in (32, 64, 128) or cfg.repeat() != 4:
             raise ValueError("the tensor-core attention serves head_dim 32/64/128 with four query heads per KV head")
+        rope_positions = int(weights.rope.shape[0])
+        if max_ctx > rope_positions:
+            raise ValueError(f"max_ctx {max_ctx} exceeds the RoPE table's {rope_positions} positions "
+                             "(the QKV epilogue reads rope[pos] for every pos < max_ctx)")
         self.max_rows = max_rows
         self.max_pages = (max_ctx + 63) // 64
         lt = (max_rows + 15) // 16

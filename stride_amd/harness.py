@@ -66,7 +66,7 @@ def best_split(best: torch.Tensor):
 @dataclass
 class PagedKv:
     """A paged KV arena in the reference layout [block][layer][K|V][group][token][dim]
-    (src/kernels.h:9, src/kv_cache.cpp:10-40), bf16 elements."""
+    (src/kernels.h:10, src/kv_cache.cpp:10-40), bf16 elements."""
 
     arena: torch.Tensor
     table: torch.Tensor

@@ -128,8 +128,14 @@ def build_rope_table(cfg: ModelConfig, max_positions: int) -> np.ndarray:
     inv = rope_frequencies(cfg)
     pos = np.arange(max_positions, dtype=np.float32)
     ang = (pos[:, None] * inv[None, :]).astype(np.float32)  # one fp32 product per entry
-    a64 = ang.astype(np.float64)
-    return np.stack([np.cos(a64), np.sin(a64)], axis=-1).astype(np.float32)
+    # cos/sin of the C library (Python's math module calls it), as std::cos and
+    # std::sin on double do; NumPy's vectorised versions may round differently
+    # depending on the host's SIMD dispatch.
+    a64 = ang.astype(np.float64).ravel().tolist()
+    cs = np.empty((len(a64), 2), np.float64)
+    cs[:, 0] = [math.cos(a) for a in a64]
+    cs[:, 1] = [math.sin(a) for a in a64]
+    return cs.astype(np.float32).reshape(max_positions, inv.size, 2)
 
 
 class Checkpoint:

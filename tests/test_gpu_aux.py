@@ -62,6 +62,27 @@ def test_norm_rows_are_batch_invariant(exact):
     assert torch.equal(part, full[perm])
 
 
+@pytest.mark.parametrize("per_lane", [True, False])
+def test_norm_tree_pinned_rows(exact, per_lane):
+    """Rows whose fp32 sum depends on the summation tree (tests/norm_tree.py):
+    the GPU output equals the oracle's, which equals the closed form of the
+    reference tree's sum, for each row at lane 0 and at lane 21 of a 23-row batch."""
+    import norm_tree
+
+    say("tc_norm pinned tree rows, per_lane", per_lane)
+    h, g, want, _ = norm_tree.pinned_inputs()
+    rng = np.random.default_rng(9)
+    for i in range(h.shape[0]):
+        batch = (rng.standard_normal((23, norm_tree.DIM)) * 3).astype(np.float32)
+        batch[0] = h[i]
+        batch[21] = h[i]
+        ht = layout.lane_tiles(torch.from_numpy(batch).to(DEV))
+        x = harness.norm(ht, 23, torch.from_numpy(g[i]).to(DEV), float(norm_tree.EPS), per_lane=per_lane)
+        got = layout.untile_lanes(x.cpu(), 23).numpy().view(np.uint16)
+        assert np.array_equal(got[0], want[i]) and np.array_equal(got[21], want[i]), f"row {i}"
+        assert np.array_equal(got, exact.tc_norm(batch, g[i], float(norm_tree.EPS)))
+
+
 def test_compact():
     say("tc_compact")
     rng = np.random.default_rng(4)

@@ -16,7 +16,7 @@ from stride_amd import harness, layout, synth
 pytestmark = pytest.mark.gpu
 
 DEV = "cuda:0"
-MS = [1, 8, 32, 64, 128, 290, 1024, 4096]
+MS = [1, 8, 32, 64, 128, 290, 1024, 1536, 2048, 4096]
 
 
 def say(*a):
@@ -129,7 +129,9 @@ def test_qkv(gen, xs):
 def test_lm_head_greedy_and_full(gen, xs):
     vocab = 128256
     w = layout.pack_tiles(rand_bf16(gen, vocab, 2048, 0.02))
-    msl = [1, 64, 128, 290]
+    # 1024 rows take the 256 x 256 pipeline blocks that serve M > 384; 290 the
+    # 128 x 256 ones; 64 and 128 the decode kernels
+    msl = [1, 64, 128, 290, 1024]
     x = xs[2048][:max(msl)]
     ref = harness.lm_greedy(w, layout.lane_tiles(x), x.shape[0], vocab)
     for m in msl:
@@ -139,13 +141,16 @@ def test_lm_head_greedy_and_full(gen, xs):
     p = _perm(128, 9)
     b = harness.lm_greedy(w, layout.lane_tiles(x[:128][p]), 128, vocab)
     assert torch.equal(b.cpu(), ref[:128][p].cpu())
-    # full logits: row hashes across M (the 16-row tile of lanes is the unit of output)
-    full_ref = layout.untile_logits(harness.lm_full(w, layout.lane_tiles(x[:128]), 128), 128, vocab)
-    for m in (1, 64):
+    # full logits: row hashes across M, the reference from M = 1024 (the 16-row
+    # tile of lanes is the unit of output)
+    full_ref = layout.untile_logits(harness.lm_full(w, layout.lane_tiles(x[:1024]), 1024), 1024, vocab)
+    ref_h = row_hashes(full_ref)
+    for m in (1, 64, 128, 400):
         say("lm_full M =", m)
         f = layout.untile_logits(harness.lm_full(w, layout.lane_tiles(x[:m]), m), m, vocab)
-        assert row_hashes(f) == row_hashes(full_ref[:m])
+        assert row_hashes(f) == ref_h[:m], f"lm_full rows differ at M={m}"
+        del f
     # the argmax kernel and the full-logits kernel agree bit for bit on the max
-    vals = full_ref.max(dim=1)
-    bv, bi = harness.best_split(ref[:128])
+    vals = full_ref[:1024].max(dim=1)
+    bv, bi = harness.best_split(ref[:1024])
     assert torch.equal(vals.values.cpu(), bv)

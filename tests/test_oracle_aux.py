@@ -109,3 +109,18 @@ def test_embed_matches_reference():
     emb = bf16_bits(rng.standard_normal((300, 128)))
     tokens = rng.integers(0, 300, 21).astype(np.int32)
     assert np.array_equal(ref.embed(emb, tokens), widen(emb[tokens]))
+
+
+def test_norm_tree_pinned(exact):
+    """The oracle's tc_norm sum follows the reference tree: on rows where the fp32
+    sum depends on the grouping (tests/norm_tree.py states each closed form and
+    the sum a wrong tree gives), its output equals the closed form of the stated
+    sum and differs from every wrong tree's."""
+    import norm_tree
+
+    h, g, want, wrong = norm_tree.pinned_inputs()
+    for i in range(h.shape[0]):
+        got = exact.tc_norm(h[i:i + 1], g[i], float(norm_tree.EPS))[0]
+        assert np.array_equal(got, want[i]), f"row {i}"
+        for name, w in wrong[i]:
+            assert not np.array_equal(got, w), f"row {i}: indistinguishable from {name}"

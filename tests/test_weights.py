@@ -123,3 +123,25 @@ def test_random_weights_shapes():
     w = weights.Weights.random(cfg, "cpu", seed=2, max_positions=8)
     assert w.embed.shape == (63, 16, 16, 16) and w.lm is w.embed
     assert w.layers[0]["q"].shape == (16, 16, 16, 16) and w.layers[0]["w2"].shape == (16, 32, 16, 16)
+
+
+@pytest.mark.parametrize("cfg", [weights.ModelConfig(), weights.ModelConfig(rope_llama3=False, rope_theta=10000.0),
+                                 weights.ModelConfig(rope_llama3=False, head_dim=128)])
+def test_rope_table_bit_equal_to_restatement(exact, cfg):
+    """The loader's RoPE table equals, bit for bit, the C restatement of the
+    reference's build_rope_table (src/model.cpp:54-88) compiled with the C
+    library's cos/sin, at 4097 positions, plain and llama3-scaled."""
+    got = weights.build_rope_table(cfg, 4097)
+    want = exact.rope_table(cfg, 4097)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_engine_rejects_context_beyond_rope_table():
+    """The QKV epilogue reads rope[pos]: an engine whose context exceeds the
+    table is refused before anything is allocated."""
+    from stride_amd import engine
+
+    cfg = weights.ModelConfig(hidden=128, mlp=256, layers=1, heads=4, kv_heads=1, head_dim=32, vocab=64)
+    w = weights.Weights.random(cfg, "cpu", seed=0, max_positions=16)
+    with pytest.raises(ValueError, match="RoPE table"):
+        engine.Engine(w, slots=1, max_ctx=17, max_rows=16)
