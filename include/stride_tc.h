@@ -224,6 +224,21 @@ int stride_tc_lm_full(const StrideTcLmFullParams* p, int lane_tiles_per_block, v
  * part of x below lo is under 2^-16 of |x|. */
 int stride_tc_gemm_f32x(const StrideTcGemmF32xParams* p, void* stream);
 
+/* No reference counterpart: stride_tc_gemm_f32x for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops that
+ * forbid hipMalloc). Same result bits as stride_tc_gemm_f32x; p->workspace must
+ * be NULL: hi and lo are staged in a 16 MiB file-scope device array (each GPU
+ * the library runs on holds one until the process ends), so
+ * 2 * 16 * lane_groups * cols must not exceed stride_tc_f32x_scratch_elems()
+ * (for example M <= 256 at K = 8192 or M <= 2048 at K = 2048); larger calls are
+ * rejected with STRIDE_TC_EINVAL. Calls that overlap on one GPU (other streams,
+ * other threads) share that array and race; order them on one stream. Nothing
+ * here calls hipMalloc or hipFree. */
+int stride_tc_gemm_f32x_noalloc(const StrideTcGemmF32xParams* p, void* stream);
+
+/* Capacity of the scratch stride_tc_gemm_f32x_noalloc stages into, in bf16 elements. */
+int stride_tc_f32x_scratch_elems(void);
+
 /* Replaces stride::tc_embed (src/kernels_tc.h:79, src/kernels_tc.cu:179-203):
  * h tile row of lane j <- the fp32 widening of embedding row tokens[j]. */
 int stride_tc_embed(const StrideTcEmbedParams* p, void* stream);

@@ -175,6 +175,8 @@ EXPORTS = (
     "stride_tc_lm_greedy",
     "stride_tc_lm_full",
     "stride_tc_gemm_f32x",
+    "stride_tc_gemm_f32x_noalloc",
+    "stride_tc_f32x_scratch_elems",
     "stride_tc_embed",
     "stride_tc_norm",
     "stride_tc_attention",
@@ -237,12 +239,15 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     lib.stride_tc_lm_greedy.argtypes = [C.POINTER(TcLmGreedyParams), C.c_int, C.c_int, vp]
     lib.stride_tc_lm_full.argtypes = [C.POINTER(TcLmFullParams), C.c_int, vp]
     lib.stride_tc_gemm_f32x.argtypes = [C.POINTER(TcGemmF32xParams), vp]
+    lib.stride_tc_gemm_f32x_noalloc.argtypes = [C.POINTER(TcGemmF32xParams), vp]
+    lib.stride_tc_f32x_scratch_elems.argtypes = []
+    lib.stride_tc_f32x_scratch_elems.restype = C.c_int
     lib.stride_tc_embed.argtypes = [C.POINTER(TcEmbedParams), vp]
     lib.stride_tc_norm.argtypes = [C.POINTER(TcNormParams), C.c_int, vp]
     lib.stride_tc_attention.argtypes = [C.POINTER(AttentionParams), vp]
     lib.stride_tc_compact.argtypes = [C.POINTER(TcCompactParams), vp]
     for name in ("stride_tc_qkv", "stride_tc_gemm_residual", "stride_tc_mlp13", "stride_tc_lm_greedy",
-                 "stride_tc_lm_full", "stride_tc_gemm_f32x", "stride_tc_embed", "stride_tc_norm", "stride_tc_attention", "stride_tc_compact",
+                 "stride_tc_lm_full", "stride_tc_gemm_f32x", "stride_tc_gemm_f32x_noalloc", "stride_tc_embed", "stride_tc_norm", "stride_tc_attention", "stride_tc_compact",
                  "stride_tc_split_count"):
         getattr(lib, name).restype = C.c_int
     lib.stride_tc_split_count.argtypes = [C.c_int32, C.c_int32]

@@ -31,6 +31,8 @@
 // All call the same chunk order, the same MFMA instruction and the same
 // epilogue functions, so every output row has the same bits for any M and any
 // configuration; run() picks the configuration from measured sweeps.
+#include <mutex>
+
 #include "tc_gemm_run.hpp"
 
 namespace stride_tc {
@@ -115,6 +117,49 @@ __global__ __launch_bounds__(256) void k_zero_f32(float* y, int64_t n) {
   else for (int64_t k = i; k < n; ++k) y[k] = 0.f;
 }
 
+// Staging of stride_tc_gemm_f32x_noalloc: the hi and lo bf16 lane tiles live in
+// this file-scope array instead of a caller workspace. Every GPU the library runs
+// on holds its own copy (16 MiB) until the process ends.
+constexpr int64_t kF32xScratchElems = int64_t{8} << 20;  // bf16 elements: hi + lo
+__device__ __align__(256) uint16_t scratch[kF32xScratchElems];
+
+// Device address of `scratch` on the current device, resolved once per device
+// with hipGetSymbolAddress (the array's name is only a host-side stand-in).
+uint16_t* f32x_scratch(std::string& why) {
+  static std::once_flag once[64];
+  static uint16_t* addr[64] = {};
+  static hipError_t err[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    why = "no current HIP device";
+    return nullptr;
+  }
+  std::call_once(once[dev], [dev] {
+    void* p = nullptr;
+    err[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    addr[dev] = err[dev] == hipSuccess ? static_cast<uint16_t*>(p) : nullptr;
+  });
+  if (!addr[dev]) why = std::string("hipGetSymbolAddress(scratch) failed: ") + hipGetErrorString(err[dev]);
+  return addr[dev];
+}
+
+// The launches of stride_tc_gemm_f32x with hi/lo staged at `hi` (2 * lane
+// elements, caller-owned or the file-scope scratch).
+int gemm_f32x_launch(const StrideTcGemmF32xParams& p, uint16_t* hi, hipStream_t st) {
+  const int64_t lane_elems = static_cast<int64_t>(p.l.lane_groups) * 16 * p.m.cols;
+  uint16_t* lo = hi + lane_elems;
+  const int64_t pieces = static_cast<int64_t>(p.l.lane_groups) * 16 * (p.m.cols / 8);
+  hipLaunchKernelGGL(k_split_f32x, dim3(static_cast<unsigned>((pieces + 255) / 256)), dim3(256), 0, st, p.x, p.l.rows,
+                     p.m.cols, p.l.lane_groups, hi, lo);
+  const int64_t y_elems = static_cast<int64_t>(p.l.lane_groups) * p.m.groups * kTileElems;
+  hipLaunchKernelGGL(k_zero_f32, dim3(static_cast<unsigned>((y_elems / 4 + 255) / 256)), dim3(256), 0, st, p.y, y_elems);
+  if (hipError_t e = hipGetLastError(); e != hipSuccess)
+    return fail(static_cast<int>(e), std::string("gemm_f32x: launch failed: ") + hipGetErrorString(e));
+  EpiResidual::Out o{p.y, p.m.groups};
+  if (int rc = run<EpiResidual>(single(p.l, hi, p.m, nullptr), o, st)) return rc;
+  return run<EpiResidual>(single(p.l, lo, p.m, nullptr), o, st);
+}
+
 }  // namespace stride_tc
 
 using namespace stride_tc;
@@ -195,20 +240,26 @@ int stride_tc_gemm_f32x(const StrideTcGemmF32xParams* p, void* stream) {
   if (!lanes_ok(p->l, why) || !mat_ok(p->m, "gemm_f32x.m", why)) return fail(STRIDE_TC_EINVAL, "gemm_f32x: " + why);
   if (!p->x || !p->y || !p->workspace) return fail(STRIDE_TC_EINVAL, "gemm_f32x: null x, y or workspace");
   if (p->l.rows == 0) return 0;
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  const int64_t lane_elems = static_cast<int64_t>(p->l.lane_groups) * 16 * p->m.cols;
-  uint16_t* hi = p->workspace;
-  uint16_t* lo = p->workspace + lane_elems;
-  const int64_t pieces = static_cast<int64_t>(p->l.lane_groups) * 16 * (p->m.cols / 8);
-  hipLaunchKernelGGL(k_split_f32x, dim3(static_cast<unsigned>((pieces + 255) / 256)), dim3(256), 0, st, p->x, p->l.rows,
-                     p->m.cols, p->l.lane_groups, hi, lo);
-  const int64_t y_elems = static_cast<int64_t>(p->l.lane_groups) * p->m.groups * kTileElems;
-  hipLaunchKernelGGL(k_zero_f32, dim3(static_cast<unsigned>((y_elems / 4 + 255) / 256)), dim3(256), 0, st, p->y, y_elems);
-  if (hipError_t e = hipGetLastError(); e != hipSuccess)
-    return fail(static_cast<int>(e), std::string("gemm_f32x: launch failed: ") + hipGetErrorString(e));
-  EpiResidual::Out o{p->y, p->m.groups};
-  if (int rc = run<EpiResidual>(single(p->l, hi, p->m, nullptr), o, st)) return rc;
-  return run<EpiResidual>(single(p->l, lo, p->m, nullptr), o, st);
+  return gemm_f32x_launch(*p, p->workspace, static_cast<hipStream_t>(stream));
 }
+
+int stride_tc_gemm_f32x_noalloc(const StrideTcGemmF32xParams* p, void* stream) {
+  std::string why;
+  if (!p) return fail(STRIDE_TC_EINVAL, "gemm_f32x_noalloc: null params");
+  if (!lanes_ok(p->l, why) || !mat_ok(p->m, "gemm_f32x_noalloc.m", why))
+    return fail(STRIDE_TC_EINVAL, "gemm_f32x_noalloc: " + why);
+  if (!p->x || !p->y) return fail(STRIDE_TC_EINVAL, "gemm_f32x_noalloc: null x or y");
+  if (p->workspace) return fail(STRIDE_TC_EINVAL, "gemm_f32x_noalloc: workspace must be null (the library's scratch is used)");
+  const int64_t need = 2 * static_cast<int64_t>(p->l.lane_groups) * 16 * p->m.cols;
+  if (need > kF32xScratchElems)
+    return fail(STRIDE_TC_EINVAL, "gemm_f32x_noalloc: 2 * 16 * lane_groups * cols = " + std::to_string(need) +
+                                      " bf16 elements exceeds the scratch of " + std::to_string(kF32xScratchElems));
+  if (p->l.rows == 0) return 0;
+  uint16_t* hi = f32x_scratch(why);
+  if (!hi) return fail(STRIDE_TC_EINVAL, "gemm_f32x_noalloc: " + why);
+  return gemm_f32x_launch(*p, hi, static_cast<hipStream_t>(stream));
+}
+
+int stride_tc_f32x_scratch_elems(void) { return static_cast<int>(kF32xScratchElems); }
 
 }  // extern "C"

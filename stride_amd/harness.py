@@ -144,6 +144,14 @@ def gemm_f32x(w_tiles, x_f32, rows: int, y_out=None, workspace=None):
     return y_out
 
 
+def gemm_f32x_noalloc(w_tiles, x_f32, rows: int, y_out):
+    """gemm_f32x through the allocation-free entry point: y_out (h-layout fp32
+    tiles, at least ceil(rows/16) lane tiles) is overwritten."""
+    p = tc.TcGemmF32xParams(lanes(rows), ptr(x_f32), mat(w_tiles), ptr(y_out), None)
+    tc.tc_gemm_f32x_noalloc(p)
+    return y_out
+
+
 def embed(emb_tiles, tokens, rows: int, dim: int, h_out=None):
     """tc_embed: lane j of fp32 h tiles <- embedding row tokens[j]."""
     lt = (rows + 15) // 16

@@ -30,7 +30,7 @@ __all__ = [
     "BestEntry", "GemmMat", "KvRef", "Lanes", "StrideTcError", "TcGemmResidualParams", "TcLmFullParams",
     "TcLmGreedyParams", "TcMlp13Params", "TcQkvParams", "tc_qkv", "tc_gemm_residual", "tc_mlp13", "tc_lm_greedy",
     "tc_lm_full", "kernel_stream", "set_kernel_stream", "mat", "lanes", "ptr", "split_count", "AttentionParams",
-    "TcCompactParams", "TcEmbedParams", "TcNormParams", "TcGemmF32xParams", "tc_gemm_f32x", "tc_embed", "tc_norm", "tc_attention", "tc_compact",
+    "TcCompactParams", "TcEmbedParams", "TcNormParams", "TcGemmF32xParams", "tc_gemm_f32x", "tc_gemm_f32x_noalloc", "tc_embed", "tc_norm", "tc_attention", "tc_compact",
 ]
 
 _stream = None  # None -> torch's current stream at call time
@@ -115,3 +115,9 @@ def tc_compact(p: TcCompactParams) -> None:
 def tc_gemm_f32x(p: TcGemmF32xParams) -> None:
     """y = W x for fp32 activations (no reference counterpart; see include/stride_tc.h)."""
     _lib.check(_lib_().stride_tc_gemm_f32x(C.byref(p), kernel_stream()))
+
+
+def tc_gemm_f32x_noalloc(p: TcGemmF32xParams) -> None:
+    """tc_gemm_f32x staged in the library's device scratch (p.workspace must be
+    null): allocates nothing, for callers that cannot allocate."""
+    _lib.check(_lib_().stride_tc_gemm_f32x_noalloc(C.byref(p), kernel_stream()))
