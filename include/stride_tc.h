@@ -13,7 +13,8 @@
  *   x / z    X[lane tile][col tile][16 lanes][16 cols] bf16
  *   h        fp32, same tile grid as x: h[lane tile][row tile][16 lanes][16 rows]
  *   logits   fp32 [row tile][lane tile][16 rows][16 lanes]
- * Shapes: cols (K) must be a multiple of 32; lane_groups must equal ceil(rows/16);
+ * Shapes: cols (K) must be a multiple of 16 (the reference's 16-column tiles,
+ * src/model.cpp:114-120); lane_groups must equal ceil(rows/16);
  * lanes past `rows` inside the last lane tile must hold zeros (the engine
  * zero-fills its tile buffers, src/engine.cpp:72-80).
  *
@@ -22,7 +23,10 @@
  * blocking hint: K is consumed in 32-column chunks in ascending order by one
  * v_mfma_f32_16x16x32_bf16 chain per split, the split count S depends only on
  * the weight shape (stride_tc_split_count), and the S partial sums combine left
- * to right, split 0 starting from the residual where there is one.
+ * to right, split 0 starting from the residual where there is one. When K is
+ * 16 (mod 32) the last split's chain ends with one more MFMA over the trailing
+ * 16 columns, whose upper 16 k are zero; such launches always run the
+ * register-streaming kernel (correct for any M, not tuned for prefill).
  *
  * Errors: every entry point returns 0 on success or a nonzero code (a hipError_t
  * value, or STRIDE_TC_EINVAL for rejected arguments); stride_tc_last_error()

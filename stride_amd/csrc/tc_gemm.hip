@@ -216,7 +216,7 @@ int stride_tc_stream_config(int32_t index, int32_t* out6) {
 }
 
 int stride_tc_split_count(int32_t n, int32_t k) {
-  if (n <= 0 || k <= 0 || k % kChunkCols != 0) return fail(-1, "split_count: need n > 0 and k a positive multiple of 32"), -1;
+  if (n <= 0 || k <= 0 || k % 16 != 0) return fail(-1, "split_count: need n > 0 and k a positive multiple of 16"), -1;
   return split_count(n, k);
 }
 

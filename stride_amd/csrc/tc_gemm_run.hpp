@@ -51,8 +51,8 @@ inline bool lanes_ok(const StrideLanes& l, std::string& why) {
 }
 
 inline bool mat_ok(const StrideGemmMat& m, const char* name, std::string& why) {
-  if (!m.w || m.groups <= 0 || m.cols <= 0 || m.cols % kChunkCols != 0) {
-    why = std::string(name) + ": need a weight pointer, groups > 0 and cols a positive multiple of 32 (groups=" +
+  if (!m.w || m.groups <= 0 || m.cols <= 0 || m.cols % 16 != 0) {
+    why = std::string(name) + ": need a weight pointer, groups > 0 and cols a positive multiple of 16 (groups=" +
           std::to_string(m.groups) + ", cols=" + std::to_string(m.cols) + ")";
     return false;
   }
@@ -191,6 +191,7 @@ inline int64_t total_tiles(const Geometry& g) {
 
 // Can configuration c serve this launch?
 inline bool decode_cfg_fits(const DecodeCfg& c, Geometry g, int smax, int mats, bool reduce) {
+  if (c.xl && (g.col_tiles & 1)) return false;  // a trailing half chunk is read from L2 only
   int u = c.u / mats > 0 ? c.u / mats : 1;
   if (c.xl) {
     const int umax = 128 / (c.ws * 2 * c.lt) > 0 ? 128 / (c.ws * 2 * c.lt) : 1;
@@ -258,6 +259,7 @@ constexpr int kDecIndexBase = 1000;
 extern int g_forced_dec;
 
 inline bool dec_cfg_fits(const DecCfg& c, const Geometry& g, int smax, int mats, bool reduce) {
+  if (g.col_tiles & 1) return false;  // whole 32-column chunks only
   const int chunks = g.col_tiles >> 1;
   if (c.xs) {
     if (reduce || smax < 2 || smax > kMaxXSplits) return false;
@@ -321,6 +323,13 @@ inline int pick_decode(int T, int smax, int mats, int nseg, int per) {
   if (T <= 2) return smax == 1 ? 7 : (smax == 2 ? 22 : 1);
   if (T <= 4) return smax == 1 ? 13 : (smax == 2 ? 27 : (nseg == 3 ? 33 : 5));
   return smax == 1 ? 16 : (smax == 2 ? 36 : (nseg == 3 ? 9 : 33));
+}
+
+// Streaming configuration (no x staging) for K = 16 (mod 32), any lane-tile count.
+inline int pick_half(int T, int smax) {
+  if (smax == 1) return T <= 1 ? 3 : 17;
+  if (smax == 2) return T <= 1 ? 2 : 6;
+  return T <= 1 ? 0 : 33;
 }
 
 template <class Epi, int WRT, int WLT>
@@ -430,6 +439,7 @@ inline bool pipe_cfg_fits(int idx, const Geometry& g) {
       STRIDE_TC_PIPE_CONFIGS(STRIDE_TC_PIPE_KC)
 #undef STRIDE_TC_PIPE_KC
   };
+  if (g.col_tiles & 1) return false;  // whole 32-column chunks only
   const int chunks = g.col_tiles >> 1;
   // An odd chunk count per stage is processed two stages at a time.
   const int step = kc[idx] % 2 ? 2 * kc[idx] : kc[idx];
@@ -543,6 +553,12 @@ int run(Geometry g, const typename Epi::Out& o_in, hipStream_t st) {
     const Pick p = T <= kStreamMaxLaneTiles ? pick_small(T, smax, Epi::kMats, g.nseg, per) : pick_large(g, T, smax, per);
     kind = p.kind;
     idx = p.idx;
+    if (g.col_tiles & 1) {
+      // K = 16 (mod 32): only the register-streaming kernel reads the trailing
+      // half chunk, so every M runs it (same expression for every row).
+      kind = 0;
+      idx = pick_half(T, smax);
+    }
     if (kind == 1 && !pipe_cfg_fits(idx, g)) {
       idx = pick_pipe(g, smax);
       if (!pipe_cfg_fits(idx, g)) idx = 0;

@@ -94,8 +94,14 @@ __device__ __forceinline__ void xs_finish(const Geometry& g, const typename Epi:
                                                kCachePolicySc1);
     }
   }
-  // The partial stores are complete (performed at device scope) before this
-  // workgroup is counted.
+  // The partial stores are complete (performed at device scope: sc1 stores
+  // write through this XCD's L2) before this workgroup is counted, and the last
+  // arriver reads them with sc1 loads, which read past its own L1 and L2. That
+  // is the ordering an agent-scope release/acquire pair would give; the pair
+  // itself is not used because on this target it also writes back and
+  // invalidates the whole L2 of the XCD (buffer_wbl2 / buffer_inv sc1), which
+  // measured +30 % on the down projection at M = 128 (18.7 -> 24.9 us) while
+  // the sc1 traffic already needs neither.
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   __shared__ int last;
@@ -105,6 +111,9 @@ __device__ __forceinline__ void xs_finish(const Geometry& g, const typename Epi:
     if (last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
+  // Compiler ordering only (no cache maintenance at workgroup scope): the
+  // partial loads below stay after the barrier that published `last`.
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
   if (!last) return;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
@@ -357,6 +366,26 @@ __global__ __launch_bounds__(kWave * WS * WR) void k_stream(Geometry g, typename
 #pragma unroll
           for (int r = 0; r < R; ++r) acc[m][r][l] = mfma(load16(wp[m][r] + static_cast<int64_t>(c) * kChunkBytes), bv, acc[m][r][l]);
       }
+    }
+  }
+
+  // K = 32 * chunks + 16: the last split ends with a half chunk, the 16 columns
+  // of column tile 2 * chunks. Lanes 0..31 hold its k 0..15 (tile 0 of a chunk's
+  // fragment layout); lanes 32..63, the MFMA's k 16..31, hold zeros. (The host
+  // only selects configurations without x staging for such K.)
+  if (__builtin_amdgcn_readfirstlane((g.col_tiles & 1) && active && my_split == splits - 1)) {
+    const u32x4 zero = {0u, 0u, 0u, 0u};
+    const int64_t tail = static_cast<int64_t>(chunks) * kChunkBytes;
+#pragma unroll
+    for (int l = 0; l < LT; ++l) {
+      const u32x4 bv = lane < 32 ? load16(xp[l] + tail) : zero;
+#pragma unroll
+      for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const u32x4 av = lane < 32 ? load16(wp[m][r] + tail) : zero;
+          acc[m][r][l] = mfma(av, bv, acc[m][r][l]);
+        }
     }
   }
 

@@ -105,11 +105,13 @@ def test_exact_struct_layout_matches_reference(tmp_path):
 
 def test_split_rule():
     cases = {(2048, 2048): 8, (3072, 2048): 8, (512, 2048): 8, (2048, 8192): 8, (8192, 2048): 2,
-             (128256, 2048): 1, (16, 64): 2, (16, 32): 1, (64, 96): 3, (64, 160): 5, (64, 192): 6}
+             (128256, 2048): 1, (16, 64): 2, (16, 32): 1, (64, 96): 3, (64, 160): 5, (64, 192): 6,
+             # K = 16 (mod 32): whole chunks decide, the half chunk joins the last split
+             (16, 48): 1, (16, 16): 1, (2048, 2064): 8, (8192, 2064): 2, (64, 112): 3}
     for (n, k), s in cases.items():
         assert tc.split_count(n, k) == s, (n, k)
     with pytest.raises(_lib.StrideTcError):
-        tc.split_count(16, 48)
+        tc.split_count(16, 24)
 
 
 def test_rejects_bad_arguments_without_launch():
@@ -117,9 +119,9 @@ def test_rejects_bad_arguments_without_launch():
     p = tc.TcGemmResidualParams(tc.Lanes(17, 1, 0, 0), 0x1000, tc.GemmMat(0x2000, 4, 64), 0x3000)
     assert lib.stride_tc_gemm_residual(C.byref(p), 1, 1, None) == _lib.EINVAL
     assert b"lane_groups" in lib.stride_tc_last_error()
-    p = tc.TcGemmResidualParams(tc.Lanes(17, 2, 0, 0), 0x1000, tc.GemmMat(0x2000, 4, 48), 0x3000)
+    p = tc.TcGemmResidualParams(tc.Lanes(17, 2, 0, 0), 0x1000, tc.GemmMat(0x2000, 4, 40), 0x3000)
     assert lib.stride_tc_gemm_residual(C.byref(p), 1, 1, None) == _lib.EINVAL
-    assert b"multiple of 32" in lib.stride_tc_last_error()
+    assert b"multiple of 16" in lib.stride_tc_last_error()
     g = tc.TcLmGreedyParams(tc.Lanes(1, 1, 0, 0), 0x1000, tc.GemmMat(0x2000, 4, 64), 65, 0x3000)
     with pytest.raises(tc.StrideTcError, match="vocab"):
         _lib.check(lib.stride_tc_lm_greedy(C.byref(g), 1, 1, None))

@@ -94,7 +94,9 @@ def test_config1_bf16_rounding_alone_fails_the_bound(exact):
 
 
 @pytest.mark.parametrize("m,n,k", [(1, 256, 2048), (5, 128, 2048), (16, 64, 8192), (17, 256, 2048), (64, 128, 2048),
-                                   (130, 128, 1024), (290, 256, 2048), (33, 48, 96)])
+                                   (130, 128, 1024), (290, 256, 2048), (33, 48, 96),
+                                   # K = 16 (mod 32): a trailing half chunk
+                                   (37, 128, 48), (1, 2048, 2064), (130, 256, 2064), (300, 64, 16)])
 def test_gemm_residual(exact, m, n, k):
     w, xb, x = make(1, m, n, k)
     h = synth.f32_normal(1, Ids.H, m, n)
@@ -114,7 +116,8 @@ def test_gemm_residual(exact, m, n, k):
     assert np.array_equal(layout.untile_lanes(ht0.cpu().numpy(), m).view(np.uint32), h.view(np.uint32))
 
 
-@pytest.mark.parametrize("m,n,k", [(1, 128, 2048), (7, 64, 2048), (64, 64, 512), (200, 64, 1024)])
+@pytest.mark.parametrize("m,n,k", [(1, 128, 2048), (7, 64, 2048), (64, 64, 512), (200, 64, 1024), (7, 64, 48),
+                                   (140, 128, 2064)])
 def test_lm_full(exact, m, n, k):
     w, xb, x = make(2, m, n, k, w_id=Ids.LM)
     say("lm_full", m, n, k)
@@ -125,7 +128,7 @@ def test_lm_full(exact, m, n, k):
     assert np.all(err <= tol_matrix(x, w)), f"max err {err.max()}"
 
 
-@pytest.mark.parametrize("m,n,k", [(1, 256, 2048), (9, 128, 2048), (128, 64, 2048), (150, 64, 512)])
+@pytest.mark.parametrize("m,n,k", [(1, 256, 2048), (9, 128, 2048), (128, 64, 2048), (150, 64, 512), (9, 128, 2064)])
 def test_mlp13(exact, m, n, k):
     w1 = synth.bf16_normal(3, Ids.W1, n, k, 0.02)
     w3 = synth.bf16_normal(3, Ids.W3, n, k, 0.02)
@@ -186,7 +189,7 @@ def test_lm_greedy_agreement(exact):
 
 
 @pytest.mark.parametrize("D,nq,nkv,k,m,page", [(64, 512, 128, 2048, 5, 64), (64, 256, 128, 2048, 40, 16),
-                                              (16, 64, 32, 256, 21, 16)])
+                                              (16, 64, 32, 256, 21, 16), (64, 256, 128, 2064, 21, 16)])
 def test_qkv(exact, D, nq, nkv, k, m, page):
     wq = synth.bf16_normal(6, Ids.WQ, nq, k, 0.02)
     wk = synth.bf16_normal(6, Ids.WK, nkv, k, 0.02)
@@ -220,3 +223,37 @@ def test_qkv(exact, D, nq, nkv, k, m, page):
     assert np.all(np.abs(vg - rv) <= tv + np.abs(rv) * 2.0 ** -8 + 1e-7), "v mismatch"
     # the other layer of the arena stays untouched
     assert int(torch.count_nonzero(kv.arena)) == 2 * m * nkv - int((kg == 0).sum() + (vg == 0).sum())
+
+
+def test_half_chunk_rows_are_batch_invariant():
+    """K = 2064 (16 mod 32): every output row has the same bits at M = 1, 37,
+    128 and 300 (the largest as the reference) and under a row permutation, for
+    the residual GEMM (8 splits) and the LM head (1 split, greedy and full)."""
+    import hashlib
+
+    n, k = 2048, 2064
+    w, xb, _ = make(8, 300, n, k)
+    wt = dev_u16(layout.pack_tiles(w))
+    h0 = synth.f32_normal(8, Ids.H, 300, n)
+
+    def res(rows):
+        ht = dev_f32(layout.lane_tiles(h0[rows]))
+        harness.gemm_residual(wt, dev_u16(layout.lane_tiles(xb[rows])), ht, len(rows))
+        return layout.untile_lanes(ht.cpu().numpy(), len(rows))
+
+    def hashes(a):
+        return [hashlib.sha256(r.tobytes()).hexdigest() for r in a]
+
+    ref = hashes(res(np.arange(300)))
+    for m in (1, 37, 128):
+        say("half-chunk residual M =", m)
+        assert hashes(res(np.arange(m))) == ref[:m], f"rows differ at M={m}"
+    p = np.random.default_rng(3).permutation(128)
+    assert hashes(res(p)) == [ref[i] for i in p]
+    wl = synth.bf16_normal(9, Ids.LM, 1000, k, 0.02)
+    wlt = dev_u16(layout.pack_tiles(wl))
+    full = harness.lm_greedy(wlt, dev_u16(layout.lane_tiles(xb)), 300, 1000).cpu()
+    for m in (1, 37, 128):
+        say("half-chunk lm_greedy M =", m)
+        b = harness.lm_greedy(wlt, dev_u16(layout.lane_tiles(xb[:m])), m, 1000).cpu()
+        assert torch.equal(b, full[:m])
