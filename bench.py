@@ -45,7 +45,8 @@ def parse():
     ap.add_argument("--cpu-threads", type=int, default=0,
                     help="threads for the CPU baseline (0: the cores this process may use, at most 16)")
     ap.add_argument("--library", type=int, default=1,
-                    help="also time torch.matmul (hipBLASLt) bf16 on the five shapes at M=4096 as context (0 to skip)")
+                    help="also time torch.matmul (hipBLASLt) bf16 on the five shapes at M=128, 2048, 4096 as context "
+                    "(0 to skip)")
     ap.add_argument("--op", default="", help="time only this GEMM (qkv, o, gate_up, down, lm_head) at --m and print "
                     "its JSON (for kernel-level profiles)")
     ap.add_argument("--engine-only", type=int, default=0,
@@ -398,29 +399,37 @@ def engine_step(torch, dev, m, steps, warmup, position=383):
                    "tc_gemm_residual), tc_norm, tc_lm_greedy"}
 
 
-def library_gemm(torch, dev, m=4096):
-    """Context for the prefill roofline: the vendor library (torch.matmul, which
-    calls hipBLASLt) on the same shapes at M = m in bf16, weights rotated past the
-    MALL, HIP-graph timing. It has no batch-invariance contract and no fused
-    epilogue, so it is a ceiling reference, not a parity target."""
+def library_gemm(torch, dev, ms=(128, 2048, 4096)):
+    """Context for both rooflines: the vendor library (torch.matmul, which calls
+    hipBLASLt) on the same shapes in bf16 (gate+up as one 16384-row matmul, no
+    SiLU), weights rotated past the MALL (at least ROTATION_BYTES per pass, as
+    the per-op table), HIP-graph timing. It has no batch-invariance contract and
+    no fused epilogue, so it is a reference point, not a parity target."""
     res = {}
     shapes = {"qkv": (3072, HIDDEN), "o": (HIDDEN, HIDDEN), "gate_up": (2 * FFN, HIDDEN), "down": (HIDDEN, FFN),
               "lm_head": (VOCAB, HIDDEN)}
-    for name, (n, k) in shapes.items():
-        a = torch.randn(m, k, device=dev, dtype=torch.bfloat16)
-        ws = [torch.randn(n, k, device=dev, dtype=torch.bfloat16) for _ in range(2 if n > 100000 else 8)]
-        g = capture(torch, [lambda w=w: torch.matmul(a, w.t()) for w in ws])
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        g.replay()
-        g.replay()
-        e1.record()
-        e1.synchronize()
-        sec = e0.elapsed_time(e1) / 1e3 / (2 * len(ws))
-        tfl = 2.0 * m * n * k / sec / 1e12
-        res[name] = {"us": round(sec * 1e6, 1), "TFLOP/s": round(tfl, 1), "frac": round(tfl / MFMA_BF16_PEAK_TFLOPS, 4)}
-        del g, ws, a
-        torch.cuda.empty_cache()
+    for m in ms:
+        row = {}
+        for name, (n, k) in shapes.items():
+            a = torch.randn(m, k, device=dev, dtype=torch.bfloat16)
+            copies = max(2, -(-ROTATION_BYTES // (2 * n * k)))
+            ws = [torch.randn(n, k, device=dev, dtype=torch.bfloat16) for _ in range(copies)]
+            g = capture(torch, [lambda w=w: torch.matmul(a, w.t()) for w in ws])
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            g.replay()
+            g.replay()
+            e1.record()
+            e1.synchronize()
+            sec = e0.elapsed_time(e1) / 1e3 / (2 * len(ws))
+            f, byt = 2.0 * m * n * k, 2.0 * n * k + 2.0 * m * k + 2.0 * m * n
+            gbs, tfl = byt / sec / 1e9, f / sec / 1e12
+            frac = gbs / HBM_PEAK_GBS if m <= 128 else tfl / MFMA_BF16_PEAK_TFLOPS
+            row[name] = {"us": round(sec * 1e6, 2), "GB/s": round(gbs, 1), "TFLOP/s": round(tfl, 1),
+                         "frac": round(frac, 4), "bound": "hbm" if m <= 128 else "mfma"}
+            del g, ws, a
+            torch.cuda.empty_cache()
+        res[str(m)] = row
     return res
 
 
@@ -527,6 +536,14 @@ def main():
 
     full = engine_step(torch, dev, a.m, a.steps, a.warmup) if a.engine else None
     library = library_gemm(torch, dev) if a.library else None
+    if library:
+        for row in table:  # vendor time / our time, same shape and M
+            lib = library.get(str(row["M"]))
+            if lib:
+                for n, v in row.items():
+                    if n in lib:
+                        v["library_us"] = lib[n]["us"]
+                        v["speedup_vs_library"] = round(lib[n]["us"] / v["us"], 3)
     threads = a.cpu_threads or cpu_threads_default()
     cpu = cpu_baseline(a.cpu_seconds, threads) if a.cpu_seconds > 0 else None
     if cpu is not None and threads != 1:
@@ -541,7 +558,7 @@ def main():
                    "step_GB/s": round(weight_bytes / (ms_step / 1e3) / 1e9, 1), "parallelism": "single-gpu",
                    "launch": "HIP graph of one step, replayed", "eager_ms_per_step": round(eager_ms, 4)},
         "roofline": roof, "cpu_baseline": cpu, "full_decode_step": full, "gemm_table": table,
-        "library_gemm_m4096": library,
+        "library_gemm": library,
     }
     print(json.dumps(out), flush=True)
 

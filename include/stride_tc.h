@@ -261,7 +261,14 @@ int stride_tc_norm(const StrideTcNormParams* p, int per_lane, void* stream);
  * then each row's pages are combined in ascending order and the output is
  * written as bf16 x tiles. The KV storage page (group_elems / head_dim tokens,
  * a power of two) is independent of the 64-position summation page. head_dim
- * must be 32, 64 or 128; n_q must be 4. */
+ * must be 32, 64 or 128; n_q must be 4.
+ * Extension (no reference counterpart): item_count == -1 means every page of
+ * every row, the list the reference's engine always builds (src/engine.cpp:
+ * 93-103); then items and scratch are not read, the page records stay in LDS and
+ * pages and combine run as one kernel (same bits). max_pages bounds the pages of
+ * a row; max_pages * (12 + 4 * head_dim) floats plus the kernel's staging must
+ * fit 159 KiB of LDS: up to 116 pages (7424 positions) at head_dim 64, 43 at
+ * head_dim 128; larger values are rejected (use an item list). */
 int stride_tc_attention(const StrideAttentionParams* p, void* stream);
 
 /* Replaces stride::tc_compact (src/kernels_tc.h:85, src/kernels_tc.cu:566-587):

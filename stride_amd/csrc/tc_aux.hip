@@ -351,6 +351,146 @@ __global__ __launch_bounds__(256) void k_attn_combine(StrideAttentionParams p) {
   }
 }
 
+// Pages and combine in one kernel, for calls that list every page of every row
+// (item_count == -1: the list the reference's engine always builds,
+// src/engine.cpp:93-103). One workgroup per (row, KV group): its NWV waves take
+// the row's 64-position pages round robin, each summing a page exactly as
+// k_attn_page does (the same expressions in the same order) into a record kept
+// in LDS; after a barrier the workgroup combines the records in ascending page
+// order exactly as k_attn_combine does and writes the bf16 x tiles. The page
+// records never leave the CU and no second launch is needed.
+template <int D, int NWV>
+__global__ __launch_bounds__(64 * NWV) void k_attn_fused(StrideAttentionParams p, int page_shift) {
+  constexpr int kEl = 8;                        // bf16 elements per 16-byte piece
+  constexpr int kPer = kAttnPage * D / kEl / 64;  // V pieces per lane
+  constexpr int kKey = D / kEl;                 // 16-byte pieces of one K row
+  constexpr int RF = 8 + kHeadsPerGroup * D;    // record floats
+  extern __shared__ float recs[];               // [pages][RF], then f[4][pages]
+  __shared__ f32x4 q4[D];
+  __shared__ f32x4 w4[NWV][kAttnPage];
+  __shared__ uint16_t vs[NWV][kAttnPage][D];
+  __shared__ float den[kHeadsPerGroup];
+  const int j = blockIdx.x / p.n_kv;
+  const int g = blockIdx.x % p.n_kv;
+  const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+  const int slot = p.row_slot[j];
+  const int visible = p.row_pos[j] + 1;
+  const int last = visible - 1;
+  const int pages = (last >> kAttnPageShift) + 1;
+  const float* qrow = p.q + static_cast<int64_t>(j) * p.q_stride + static_cast<int64_t>(g * kHeadsPerGroup) * D;
+  for (int d = t; d < D; d += 64 * NWV) q4[d] = f32x4{qrow[d], qrow[D + d], qrow[2 * D + d], qrow[3 * D + d]};
+  const float neg_inf = f32_of(0xFF800000u);
+  const int rounds = (pages + NWV - 1) / NWV;  // the same for every wave: barriers stay uniform
+  for (int it = 0; it < rounds; ++it) {
+    const int page = it * NWV + wave;
+    const bool active = page < pages;
+    const int p0 = page << kAttnPageShift;
+    const int n = active ? min(visible - p0, kAttnPage) : 0;
+    u32x4 vr[kPer], kr[kKey];
+    if (active) {
+#pragma unroll
+      for (int k = 0; k < kPer; ++k) {
+        const int P = k * 64 + lane, i = P / (D / kEl), c = P % (D / kEl);
+        vr[k] = load16(kv_row<uint16_t>(p.kv, page_shift, p.layer, 1, g, slot, min(p0 + i, last)) + c * kEl);
+      }
+      const uint16_t* key = kv_row<uint16_t>(p.kv, page_shift, p.layer, 0, g, slot, min(p0 + lane, last));
+#pragma unroll
+      for (int c = 0; c < kKey; ++c) kr[c] = load16(key + kEl * c);
+#pragma unroll
+      for (int k = 0; k < kPer; ++k) {
+        const int P = k * 64 + lane;
+        *reinterpret_cast<u32x4*>(&vs[wave][P / (D / kEl)][(P % (D / kEl)) * kEl]) = vr[k];
+      }
+    }
+    __syncthreads();  // q4 (first round) and this wave's V rows
+    f32x4 mx = {0.f, 0.f, 0.f, 0.f};
+    if (active) {
+      float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+#pragma unroll
+      for (int c = 0; c < kKey; ++c) {
+#pragma unroll
+        for (int e = 0; e < kEl; ++e) {
+          const float k = f32_of(e & 1 ? kr[c][e >> 1] & 0xFFFF0000u : kr[c][e >> 1] << 16);
+          const f32x4 qd = q4[kEl * c + e];
+          a0 = __builtin_fmaf(qd[0], k, a0);
+          a1 = __builtin_fmaf(qd[1], k, a1);
+          a2 = __builtin_fmaf(qd[2], k, a2);
+          a3 = __builtin_fmaf(qd[3], k, a3);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      float sc[kHeadsPerGroup] = {a0 * p.scale, a1 * p.scale, a2 * p.scale, a3 * p.scale};
+#pragma unroll
+      for (int h = 0; h < kHeadsPerGroup; ++h) {
+        if (lane >= n) sc[h] = neg_inf;
+        float m = sc[h];
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+          const float o = __shfl_xor(m, off);
+          if (o > m) m = o;
+        }
+        mx[h] = m;
+      }
+      if (lane < n)
+        w4[wave][lane] = f32x4{det_exp(sc[0] - mx[0]), det_exp(sc[1] - mx[1]), det_exp(sc[2] - mx[2]), det_exp(sc[3] - mx[3])};
+    }
+    __syncthreads();  // this wave's weights
+    if (active) {
+      float* rec = recs + page * RF;
+      const float* wflat = reinterpret_cast<const float*>(w4[wave]);
+      float dn = 0.0f;  // head (lane & 3)
+#pragma unroll
+      for (int itd = 0; itd < (D + 63) / 64; ++itd) {
+        const int d = lane + 64 * itd;
+        if (d >= D) continue;
+        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 4
+        for (int i = 0; i < n; ++i) {
+          const float v = f32_of(static_cast<uint32_t>(vs[wave][i][d]) << 16);
+          const f32x4 wi = w4[wave][i];
+#pragma unroll
+          for (int h = 0; h < kHeadsPerGroup; ++h) acc[h] = __builtin_fmaf(wi[h], v, acc[h]);
+          if (itd == 0) dn = dn + wflat[i * kHeadsPerGroup + (lane & 3)];
+        }
+#pragma unroll
+        for (int h = 0; h < kHeadsPerGroup; ++h) rec[8 + h * D + d] = acc[h];
+      }
+      if (lane < kHeadsPerGroup) {
+        rec[lane] = mx[lane];
+        rec[4 + lane] = dn;
+      }
+    }
+    __syncthreads();  // the staging buffers are reused by the next round
+  }
+  // Combine in ascending page order (k_attn_combine's expressions).
+  float* f = recs + pages * RF;
+  if (t < kHeadsPerGroup) {
+    float m = neg_inf;
+    for (int c = 0; c < pages; ++c) {
+      const float mc = recs[c * RF + t];
+      if (mc > m) m = mc;
+    }
+    float d = 0.0f;
+    for (int c = 0; c < pages; ++c) {
+      const float e = det_exp(recs[c * RF + t] - m);
+      f[t * pages + c] = e;
+      d = __builtin_fmaf(e, recs[c * RF + 4 + t], d);
+    }
+    den[t] = d;
+  }
+  __syncthreads();
+  const int col_tiles = p.out_cols >> 4;
+  uint16_t* out = static_cast<uint16_t*>(p.out);
+  const int64_t lane0 = static_cast<int64_t>(j >> 4) * col_tiles * kTileElems + (j & 15) * 16;
+  for (int hd = t; hd < kHeadsPerGroup * D; hd += 64 * NWV) {
+    const int qh = hd / D, d = hd % D;
+    float acc = 0.0f;
+    for (int c = 0; c < pages; ++c) acc = __builtin_fmaf(f[qh * pages + c], recs[c * RF + 8 + qh * D + d], acc);
+    const int idx = (g * kHeadsPerGroup + qh) * D + d;
+    out[lane0 + static_cast<int64_t>(idx >> 4) * kTileElems + (idx & 15)] = static_cast<uint16_t>(bf16_rne(acc / den[qh]));
+  }
+}
+
 bool lanes_valid(const StrideLanes& l) { return l.rows >= 0 && l.lane_groups == (l.rows + 15) / 16; }
 
 }  // namespace
@@ -382,6 +522,34 @@ static int combine(dim3 grid, size_t lds, hipStream_t st, const StrideAttentionP
   }
   hipLaunchKernelGGL((k_attn_combine<D, kExact>), grid, dim3(256), lds, st, p);
   return launched("attention (combine)");
+}
+
+// One-kernel attention (item_count == -1); its static LDS (staging for four
+// waves) and the row's records share the 160 KiB.
+template <int D, int NWV>
+static int fused_nwv(dim3 grid, size_t lds, hipStream_t st, const StrideAttentionParams& p, int page_shift) {
+  constexpr size_t kStatic = D * 16 + NWV * 64 * 16 + NWV * 64 * D * 2 + 64;
+  if (lds + kStatic > kCombineLdsMax)
+    return fail(STRIDE_TC_EINVAL, "tc_attention: max_pages too large for the one-kernel form (use an item list)");
+  static size_t raised = 64 * 1024;
+  if (lds > raised) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn_fused<D, NWV>),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    if (e != hipSuccess) return fail(static_cast<int>(e), std::string("tc_attention: raising the LDS limit failed: ") + hipGetErrorString(e));
+    raised = lds;
+  }
+  hipLaunchKernelGGL((k_attn_fused<D, NWV>), grid, dim3(64 * NWV), lds, st, p, page_shift);
+  return launched("attention (one kernel)");
+}
+
+// Waves per workgroup of the one-kernel form, from measurements of the full
+// decode step at position 383 (six pages per row): with many (row, group)
+// workgroups (batch 128, 1024 of them) two waves per workgroup keep more
+// workgroups resident; with fewer (batch 64) four waves finish a row sooner.
+template <int D>
+static int fused(dim3 grid, size_t lds, hipStream_t st, const StrideAttentionParams& p, int page_shift) {
+  if (grid.x >= 768) return fused_nwv<D, 2>(grid, lds, st, p, page_shift);
+  return fused_nwv<D, 4>(grid, lds, st, p, page_shift);
 }
 
 static int launched(const char* what) {
@@ -442,17 +610,27 @@ static int attention(const StrideAttentionParams* p, void* stream, const char* n
     why = kExact ? "need rows >= 0 and stride >= rows" : "lane_groups must equal ceil(rows/16)";
   else if ((D != 32 && D != 64 && D != 128) || p->kv.head_dim != D) why = "head_dim must be 32, 64 or 128 and match kv.head_dim";
   else if (p->n_q != kHeadsPerGroup) why = "four query heads per KV group are required (the reference packs them in a float4)";
-  else if (p->n_kv <= 0 || p->rec_floats < 8 + 4 * D || p->max_pages <= 0 || p->item_count < 0) why = "bad n_kv, rec_floats, max_pages or item_count";
+  else if (p->n_kv <= 0 || p->rec_floats < 8 + 4 * D || p->max_pages <= 0 || p->item_count < (kExact ? 0 : -1))
+    why = "bad n_kv, rec_floats, max_pages or item_count";
   else if (page_tokens <= 0 || (int64_t{1} << page_shift) != page_tokens) why = "the KV storage page (group_elems / head_dim) must be a power of two";
   else if (!kExact && (p->out_cols % 16 != 0 || p->out_cols < p->n_kv * p->n_q * D)) why = "out_cols must be a multiple of 16 covering every head";
-  else if (p->l.rows > 0 && (!p->q || !p->out || !p->kv.arena || !p->kv.table || !p->row_slot || !p->row_pos || !p->scratch ||
-                             (p->item_count > 0 && !p->items)))
+  else if (p->l.rows > 0 && (!p->q || !p->out || !p->kv.arena || !p->kv.table || !p->row_slot || !p->row_pos ||
+                             (p->item_count >= 0 && !p->scratch) || (p->item_count > 0 && !p->items)))
     why = "missing pointer";
   else if (static_cast<size_t>(p->max_pages) * (p->rec_floats + kHeadsPerGroup) * sizeof(float) > kCombineLdsMax)
     why = "max_pages * rec_floats too large for the combine's LDS (159 KiB)";
   if (!why.empty()) return fail(STRIDE_TC_EINVAL, std::string(name) + ": " + why);
   if (p->l.rows == 0) return 0;
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if constexpr (!kExact) {
+    if (p->item_count == -1) {
+      const size_t lds = static_cast<size_t>(p->max_pages) * (8 + 4 * D + kHeadsPerGroup) * sizeof(float);
+      const dim3 grid(p->l.rows * p->n_kv);
+      if (D == 32) return fused<32>(grid, lds, st, *p, page_shift);
+      if (D == 64) return fused<64>(grid, lds, st, *p, page_shift);
+      return fused<128>(grid, lds, st, *p, page_shift);
+    }
+  }
   using KvT = typename std::conditional<kExact, float, uint16_t>::type;
   if (p->item_count > 0) {
     const dim3 grid(p->item_count * p->n_kv);

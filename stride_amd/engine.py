@@ -77,7 +77,7 @@ class Engine:
     """One model, a paged bf16 KV cache and the step buffers for up to max_rows rows."""
 
     def __init__(self, weights: Weights, slots: int, max_ctx: int, max_rows: int, page_tokens: int = 16,
-                 shuffle_seed: int = 0):
+                 shuffle_seed: int = 0, attention_one_kernel: bool = True):
         self.w = weights
         cfg = self.cfg = weights.cfg
         dev = self.dev = weights.embed.device
@@ -88,6 +88,9 @@ class Engine:
             raise ValueError(f"max_ctx {max_ctx} exceeds the RoPE table's {rope_positions} positions "
                              "(the QKV epilogue reads rope[pos] for every pos < max_ctx)")
         self.max_rows = max_rows
+        # every step lists every page of every row, so attention can run pages and
+        # combine as one kernel (item_count = -1); False keeps the item list
+        self.one_kernel = attention_one_kernel
         self.max_pages = (max_ctx + 63) // 64
         lt = (max_rows + 15) // 16
         H, D = cfg.hidden, cfg.head_dim
@@ -116,7 +119,8 @@ class Engine:
             harness.qkv(L["q"], L["k"], L["v"], self.x, n, cfg.head_dim, w.rope, slot, pos, self.kv, layer=li,
                         q_out=self.q)
             harness.attention(self.q[:n], self.kv, slot, pos, cfg.kv_heads, cfg.head_dim, scale, layer=li,
-                              max_pages=self.max_pages, out_tiles=self.attn, items=items, scratch=self.scratch)
+                              max_pages=self.max_pages, out_tiles=self.attn, items=items, scratch=self.scratch,
+                              one_kernel=self.one_kernel)
             harness.gemm_residual(L["o"], self.attn, self.h, n)
             harness.norm(self.h, n, L["norm_mlp"], cfg.rms_eps, x_out=self.x)
             harness.mlp13(L["w1"], L["w3"], self.x, n, out=self.z)

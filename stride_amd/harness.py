@@ -190,12 +190,26 @@ def compact(in_tiles, lm_rows, out_tiles=None):
 
 
 def attention(q, kv: PagedKv, row_slot, row_pos, n_kv: int, head_dim: int, scale: float, layer: int = 0,
-              max_pages: int = 32, out_tiles=None, items=None, scratch=None):
+              max_pages: int = 32, out_tiles=None, items=None, scratch=None, one_kernel: bool = False):
     """tc_attention over every page of every row (as the engine's item list,
-    src/engine.cpp:93-103). q: [rows][n_kv*4*head_dim] fp32. Returns bf16 x tiles."""
+    src/engine.cpp:93-103). q: [rows][n_kv*4*head_dim] fp32. Returns bf16 x tiles.
+    one_kernel: pass item_count = -1 (every page of every row), which runs pages
+    and combine in one kernel with the records in LDS (no item list, no scratch)."""
     rows = int(q.shape[0])
     cols = n_kv * 4 * head_dim
     dev = q.device
+    if one_kernel:
+        if out_tiles is None:
+            out_tiles = torch.zeros(((rows + 15) // 16, cols // 16, 16, 16), dtype=U16, device=dev)
+        p = tc.AttentionParams()
+        p.l = lanes(rows)
+        p.q, p.q_stride, p.out, p.out_cols = ptr(q), cols, ptr(out_tiles), cols
+        p.kv = kv.ref
+        p.row_slot, p.row_pos, p.items, p.item_count = ptr(row_slot), ptr(row_pos), None, -1
+        p.scratch, p.max_pages, p.rec_floats = None, max_pages, 4 * head_dim + 8
+        p.layer, p.n_kv, p.n_q, p.head_dim, p.scale = layer, n_kv, 4, head_dim, scale
+        tc.tc_attention(p)
+        return out_tiles
     if items is None:
         pos = row_pos.cpu().tolist()
         items = torch.tensor([[j, pg] for j in range(rows) for pg in range((pos[j] >> 6) + 1)], dtype=torch.int32,

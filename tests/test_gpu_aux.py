@@ -96,7 +96,8 @@ def test_compact():
 
 
 @pytest.mark.parametrize("page_tokens,n_kv,hd,cap,m", [(16, 8, 64, 320, 21), (64, 8, 64, 320, 21),
-                                                        (16, 2, 128, 2048, 3), (32, 1, 32, 200, 9)])
+                                                        (16, 2, 128, 2048, 3), (32, 1, 32, 200, 9),
+                                                        (16, 8, 64, 512, 130)])
 def test_attention(exact, page_tokens, n_kv, hd, cap, m):
     say("tc_attention page_tokens", page_tokens, "n_kv", n_kv, "hd", hd, "cap", cap, "m", m)
     rng = np.random.default_rng(5 + page_tokens + hd)
@@ -116,6 +117,13 @@ def test_attention(exact, page_tokens, n_kv, hd, cap, m):
     got = layout.untile_lanes(out, m).cpu().numpy().view(np.uint16)
     want = exact.tc_attention(q, k, v, slot, pos, scale)
     assert np.array_equal(got, want), f"{(got != want).sum()} mismatches"
+    # the one-kernel form (item_count = -1: every page of every row) gives the same bits
+    say("tc_attention one kernel")
+    one = harness.attention(torch.from_numpy(q.reshape(m, -1)).to(DEV), kv, torch.from_numpy(slot).to(DEV),
+                            torch.from_numpy(pos).to(DEV), n_kv, hd, scale, layer=1, max_pages=(cap + 63) // 64,
+                            one_kernel=True)
+    got1 = layout.untile_lanes(one, m).cpu().numpy().view(np.uint16)
+    assert np.array_equal(got1, want), f"one kernel: {(got1 != want).sum()} mismatches"
 
 
 def test_attention_rejects_bad_arguments():
