@@ -320,9 +320,9 @@ inline int pick_decode(int T, int smax, int mats, int nseg, int per) {
     if (smax == 2) return 34;
     return nseg == 1 && per >= 32 ? 53 : 0;  // long splits: one split per workgroup
   }
-  if (T <= 2) return smax == 1 ? 7 : (smax == 2 ? 22 : 1);
+  if (T <= 2) return smax == 1 ? 7 : (smax == 2 ? 22 : (nseg == 3 ? 5 : 0));
   if (T <= 4) return smax == 1 ? 13 : (smax == 2 ? 27 : (nseg == 3 ? 33 : 5));
-  return smax == 1 ? 16 : (smax == 2 ? 36 : (nseg == 3 ? 9 : 33));
+  return smax == 1 ? 16 : (smax == 2 ? 36 : (nseg == 3 ? 27 : 33));
 }
 
 // Streaming configuration (no x staging) for K = 16 (mod 32), any lane-tile count.
@@ -475,17 +475,20 @@ struct Pick {
   int kind, idx;
 };
 
-// At most 8 lane tiles. At three or four lane tiles the register-streamed
-// kernel with an activation ring wins for the LM head and (two split groups per
-// workgroup) for the paired gate/up GEMM; otherwise the LDS-pipelined kernel
-// with small blocks wins for the LM head from two lane tiles up and for gate/up
-// from three.
+// At most 8 lane tiles (sweeps with every weight set rotated past the MALL, at
+// least 512 MiB per pass). The register-streamed kernel with an activation ring
+// wins for the LM head at up to four and at eight lane tiles, for the paired
+// gate/up GEMM at two to four (two split groups per workgroup) and for down at
+// two to four (one split per workgroup); otherwise the LDS-pipelined kernel with
+// small blocks wins for the LM head and for gate/up from five lane tiles.
 inline Pick pick_small(int T, int smax, int mats, int nseg, int per) {
+  if (smax == 1 && T <= 2) return {3, 10};
   if (smax == 1 && T >= 3 && T <= 4) return {3, 8};
+  if (smax == 1 && T == 8) return {3, 12};
   if (smax == 1 && T >= 2) return {1, T <= 4 ? 14 : 8};
-  if (smax == 2 && mats == 2 && T >= 3 && T <= 4) return {3, 13};
+  if (smax == 2 && mats == 2 && T >= 2 && T <= 4) return {3, 13};
   if (smax == 2 && mats == 2 && T >= 3) return {1, 15};
-  if (smax == 8 && nseg == 1 && per >= 32 && T == 4) return {3, 7};  // long splits (down), one split per workgroup
+  if (smax == 8 && nseg == 1 && per >= 32 && T >= 2 && T <= 4) return {3, 7};  // long splits (down), one split per workgroup
   return {0, pick_decode(T, smax, mats, nseg, per)};
 }
 
