@@ -334,3 +334,19 @@ extern "C" double ref_bench_gemm(const uint16_t* w, int n, int k, const float* x
   const auto t1 = std::chrono::steady_clock::now();
   return std::chrono::duration<double>(t1 - t0).count();
 }
+
+// The reference's exact-path entry points themselves, taking its own parameter
+// blocks (pointers into host memory: the CPU build's "device" is the host). An
+// exact-path engine step driven through these on the CPU is the reference's
+// Engine::step_exact (src/engine.cpp:144-297) operator for operator.
+extern "C" {
+void ref_k_embed(const EmbedParams* p) { k_embed(*p); }
+void ref_k_norm(const NormParams* p, int J) { k_norm(*p, J); }
+void ref_k_qkv(const QkvParams* p, int J) { k_qkv(*p, J); }
+void ref_k_attention(const AttentionParams* p) { k_attention(*p); }
+void ref_k_gemm_residual(const GemmResidualParams* p, int J) { k_gemm_residual(*p, J); }
+void ref_k_mlp13(const Mlp13Params* p, int J) { k_mlp13(*p, J); }
+void ref_k_compact(const CompactParams* p) { k_compact(*p); }
+void ref_k_lm_greedy(const LmGreedyParams* p, int J) { k_lm_greedy(*p, J); }
+void ref_k_lm_full(const LmFullParams* p, int J) { k_lm_full(*p, J); }
+}  // extern "C"

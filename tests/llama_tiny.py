@@ -56,9 +56,11 @@ def bf16(a):
     return r.view(np.float32).astype(np.float64)
 
 
-def forward_last_logits(t, c, tokens, rope):
+def forward_last_logits(t, c, tokens, rope, round_bf16=True):
     """Logits (float64) of the last position of `tokens` for one sequence.
-    rope: [pos][D/2][cos, sin]. RoPE rotates pairs (i, i + D/2)."""
+    rope: [pos][D/2][cos, sin]. RoPE rotates pairs (i, i + D/2). round_bf16=False
+    keeps every intermediate in float64 (the exact path stores fp32 throughout)."""
+    bf16 = globals()["bf16"] if round_bf16 else (lambda a: np.asarray(a, np.float64))
     H, D = c["hidden_size"], c["head_dim"]
     nq, nkv, eps = c["num_attention_heads"], c["num_key_value_heads"], c["rms_norm_eps"]
     n = len(tokens)
