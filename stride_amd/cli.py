@@ -1,9 +1,14 @@
 """Greedy batch driver with a run ledger, the counterpart of the reference's
-tools/stride_cli.cpp on the tensor-core path:
+tools/stride_cli.cpp:
 
     python -m stride_amd.cli --model DIR --input prompts.jsonl --output out.jsonl
-        [--max-new N] [--concurrency C] [--max-rows R] [--page-tokens P]
-        [--kv-shuffle S] [--row-shuffle S] [--use-eos]
+        [--path tc|exact] [--max-new N] [--concurrency C] [--max-rows R]
+        [--page-tokens P] [--kv-shuffle S] [--row-shuffle S] [--use-eos]
+
+--path tc (default) runs the tensor-core operators (bf16 tiles, bf16 KV in
+--page-tokens pages); --path exact runs the exact FP32 path
+(stride_amd.exact_engine: fp32 activations and KV in 64-token blocks), whose
+ledger is the reference's exact-path ledger bit for bit on the same weights.
 
 Input lines: {"id": 0, "tokens": [1, 2, 3]}. Output lines (one per prompt, in
 input order): {"id": 0, "tokens": [...], "values": ["3f800000", ...],
@@ -45,6 +50,27 @@ def fingerprint(tokens, values) -> int:
     for t, v in zip(tokens, values):
         h = engine.fnv_mix(engine.fnv_mix(h, t), v)
     return h
+
+
+class _ExactSlots:
+    def __init__(self, slots, capacity):
+        self.slots, self.capacity = slots, capacity
+
+
+class ExactCliEngine:
+    """The exact-path engine behind the Scheduler's interface (step(rows, greedy)
+    -> [(index, value bits)], kv.slots, kv.capacity, max_rows)."""
+
+    def __init__(self, model, slots: int, max_ctx: int, max_rows: int, shuffle_seed: int, device: str):
+        from . import exact_engine
+
+        self.inner = exact_engine.ExactEngine(model, exact_engine.GpuBackend(device), slots, max_ctx, max_rows,
+                                              shuffle_seed)
+        self.kv = _ExactSlots(slots, max_ctx)
+        self.max_rows = max_rows
+
+    def step(self, rows, greedy):
+        return self.inner.step(rows, greedy=greedy)[0]
 
 
 class Scheduler:
@@ -127,6 +153,7 @@ def main(argv=None) -> int:
     ap.add_argument("--row-shuffle", type=int, default=0)
     ap.add_argument("--use-eos", action="store_true")
     ap.add_argument("--device", default="cuda:0")
+    ap.add_argument("--path", choices=("tc", "exact"), default="tc")
     a = ap.parse_args(argv)
 
     import torch
@@ -138,13 +165,24 @@ def main(argv=None) -> int:
     with open(a.input) as f:
         prompts = [(int(j["id"]), [int(t) for t in j["tokens"]]) for j in map(json.loads, filter(str.strip, f))]
     longest = max(len(t) for _, t in prompts) + a.max_new
-    if a.model.startswith("random:"):
-        w = weights.Weights.random(weights.ModelConfig(), a.device, int(a.model.split(":", 1)[1]), longest + 1)
+    if a.path == "exact":
+        from . import exact_engine
+
+        if a.model.startswith("random:"):
+            model = exact_engine.ExactModel.random(weights.ModelConfig(), int(a.model.split(":", 1)[1]), longest + 1)
+        else:
+            model = exact_engine.ExactModel.load(a.model, max_positions=longest + 1)
+        eng = ExactCliEngine(model, a.concurrency, longest, a.max_rows, a.kv_shuffle, a.device)
+        cfg = model.cfg
     else:
-        w = weights.Weights.load(a.model, a.device, max_positions=longest + 1)
-    eng = engine.Engine(w, slots=a.concurrency, max_ctx=longest, max_rows=a.max_rows, page_tokens=a.page_tokens,
-                        shuffle_seed=a.kv_shuffle)
-    eos = w.cfg.eos_tokens if a.use_eos else ()
+        if a.model.startswith("random:"):
+            w = weights.Weights.random(weights.ModelConfig(), a.device, int(a.model.split(":", 1)[1]), longest + 1)
+        else:
+            w = weights.Weights.load(a.model, a.device, max_positions=longest + 1)
+        eng = engine.Engine(w, slots=a.concurrency, max_ctx=longest, max_rows=a.max_rows, page_tokens=a.page_tokens,
+                            shuffle_seed=a.kv_shuffle)
+        cfg = w.cfg
+    eos = cfg.eos_tokens if a.use_eos else ()
     done = Scheduler(eng, a.concurrency, a.max_new, eos, a.row_shuffle).run(prompts)
     with open(a.output, "w") as f:
         for line in ledger_lines(prompts, done):

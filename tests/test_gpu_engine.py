@@ -83,7 +83,8 @@ def test_loaded_checkpoint_matches_float64_forward(tmp_path, tied):
     assert s1.tokens == seqs[2].tokens and s1.values == seqs[2].values and s1.fingerprint == seqs[2].fingerprint
 
 
-def test_ledger_identical_across_scheduling(tmp_path):
+@pytest.mark.parametrize("path", ["tc", "exact"])
+def test_ledger_identical_across_scheduling(tmp_path, path):
     """stride_amd.cli on a tiny checkpoint: the JSONL ledger (tokens, logit bits,
     fingerprints) must be byte-identical whether sequences run one at a time or
     three at a time with a 16-row budget (prompts split across steps), shuffled
@@ -99,11 +100,11 @@ def test_ledger_identical_across_scheduling(tmp_path):
             f.write(json.dumps({"id": 10 + i, "tokens": rng.integers(0, 1000, n).tolist()}) + "\n")
     say("ledger: sequential")
     assert cli.main(["--model", str(tmp_path / "m"), "--input", str(tmp_path / "p.jsonl"), "--output",
-                     str(tmp_path / "a.jsonl"), "--max-new", "6"]) == 0
+                     str(tmp_path / "a.jsonl"), "--max-new", "6", "--path", path]) == 0
     say("ledger: batched")
     assert cli.main(["--model", str(tmp_path / "m"), "--input", str(tmp_path / "p.jsonl"), "--output",
                      str(tmp_path / "b.jsonl"), "--max-new", "6", "--concurrency", "3", "--max-rows", "16",
-                     "--row-shuffle", "5", "--kv-shuffle", "7"]) == 0
+                     "--row-shuffle", "5", "--kv-shuffle", "7", "--path", path]) == 0
     a, b = (tmp_path / "a.jsonl").read_text(), (tmp_path / "b.jsonl").read_text()
     assert a == b
     recs = [json.loads(line) for line in a.splitlines()]
