@@ -34,11 +34,15 @@
  * `stream` (NULL = the default stream); nothing here synchronizes or allocates.
  *
  * Shared device state: GEMM launches that combine splits across workgroups, and
- * the greedy LM head, use one 16 MiB device-global scratch array and a set of
- * arrival counters per device. Launches on one device must therefore be ordered
- * (one stream, as the reference keeps them, src/kernels.cu:457-460); launches
- * that overlap on one device race. The configuration hooks below are
- * process-wide and meant for tuning sweeps, not for concurrent callers.
+ * the greedy LM head, use a 16 MiB device-global scratch array and a set of
+ * arrival counters. There are four such sets per device, each bound to the
+ * stream that last used it (a new stream takes a free set, else the least
+ * recently used one), so launches on up to four streams of one device may
+ * overlap; with more streams in flight at once, order them (the reference
+ * keeps every launch on one stream, src/kernels.cu:457-460). A launch captured
+ * in a HIP graph keeps the set of its capture stream. The configuration hooks
+ * below are process-wide and meant for tuning sweeps, not for concurrent
+ * callers.
  */
 #ifndef STRIDE_TC_H
 #define STRIDE_TC_H

@@ -44,37 +44,56 @@ int fail(int code, const std::string& msg) {
   return code;
 }
 
-// One device scratch array (partials of cross-workgroup split launches or the
-// greedy LM head's candidates) and the split arrival counters; their addresses
-// come from hipGetSymbolAddress once per device, so no entry point allocates.
-__device__ __align__(256) unsigned long long g_scratch[kScratchBytes / 8];
+// Device scratch for the split partials of cross-workgroup split launches and
+// the greedy LM head's candidates, with the split arrival counters: kScratchSets
+// file-scope sets, so no entry point allocates. Each stream that launches such
+// kernels is given a set of its own (the first free set, else the set its device
+// used least recently), so launches on up to kScratchSets streams of one device
+// may overlap; ordering is only needed beyond that. Counters are left at zero by
+// every launch. Addresses come from hipGetSymbolAddress once per device.
+__device__ __align__(256) unsigned long long g_scratch[kScratchSets][kScratchBytes / 8];
+__device__ __align__(256) int32_t g_split_cnt[kScratchSets][kSplitUnits];
 
-// Arrival counters of cross-workgroup split launches, one per (row block, lane
-// group) unit; each launch leaves them at zero.
-__device__ __align__(256) int32_t g_split_cnt[kSplitUnits];
+namespace {
+struct DeviceScratch {
+  unsigned long long* scratch = nullptr;
+  int32_t* counters = nullptr;
+  hipStream_t owner[kScratchSets] = {};
+  bool used[kScratchSets] = {};
+  uint64_t last_use[kScratchSets] = {};
+  uint64_t tick = 0;
+};
+std::mutex g_scratch_mu;
+DeviceScratch g_dev_scratch[64];
+}  // namespace
 
-int32_t* split_counters() {
-  static int32_t* cache[64] = {};
+ScratchSet scratch_for(hipStream_t st) {
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
-  if (!cache[dev]) {
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return {};
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  DeviceScratch& d = g_dev_scratch[dev];
+  if (!d.scratch) {
     void* p = nullptr;
-    if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_split_cnt)) != hipSuccess) return nullptr;
-    cache[dev] = static_cast<int32_t*>(p);
+    void* c = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_scratch)) != hipSuccess) return {};
+    if (hipGetSymbolAddress(&c, HIP_SYMBOL(g_split_cnt)) != hipSuccess) return {};
+    d.scratch = static_cast<unsigned long long*>(p);
+    d.counters = static_cast<int32_t*>(c);
   }
-  return cache[dev];
-}
-
-unsigned long long* scratch_base() {
-  static unsigned long long* cache[64] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
-  if (!cache[dev]) {
-    void* p = nullptr;
-    if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_scratch)) != hipSuccess) return nullptr;
-    cache[dev] = static_cast<unsigned long long*>(p);
+  int pick = -1;
+  for (int i = 0; i < kScratchSets && pick < 0; ++i)
+    if (d.used[i] && d.owner[i] == st) pick = i;
+  for (int i = 0; i < kScratchSets && pick < 0; ++i)
+    if (!d.used[i]) pick = i;
+  if (pick < 0) {
+    pick = 0;
+    for (int i = 1; i < kScratchSets; ++i)
+      if (d.last_use[i] < d.last_use[pick]) pick = i;
   }
-  return cache[dev];
+  d.used[pick] = true;
+  d.owner[pick] = st;
+  d.last_use[pick] = ++d.tick;
+  return {d.scratch + static_cast<int64_t>(pick) * (kScratchBytes / 8), d.counters + static_cast<int64_t>(pick) * kSplitUnits};
 }
 
 int g_forced_cfg = -1;

@@ -138,19 +138,22 @@ constexpr int kNumDecodeCfgs = sizeof(kDecodeCfgs) / sizeof(kDecodeCfgs[0]);
 
 extern int g_forced_cfg;
 
-// Device scratch shared by two uses: the greedy LM head's argmax candidates
-// (one 8-byte (value, index) slot per (row block, batch lane)) and the fp32
-// split partials of cross-workgroup split launches. A fixed file-scope device
-// array, so the entry points allocate nothing; launches on one device share it
-// and must be ordered on one stream (the reference keeps every launch on one
-// stream, src/kernels.cu:457-460).
+// Device scratch for two uses: the greedy LM head's argmax candidates (one
+// 8-byte (value, index) slot per (row block, batch lane)) and the fp32 split
+// partials of cross-workgroup split launches. Fixed file-scope device arrays, so
+// the entry points allocate nothing; one set per stream (scratch_for), so
+// launches on up to kScratchSets streams of a device may run concurrently.
 constexpr int64_t kScratchBytes = int64_t{16} << 20;
 constexpr int64_t kCandSlots = kScratchBytes / 8;
 constexpr int kSplitUnits = 1 << 16;  // arrival counters of cross-workgroup split launches
 
-// Device addresses of the file-scope scratch and counters (resolved once per device).
-int32_t* split_counters();
-unsigned long long* scratch_base();
+// Scratch sets: a launch on stream st uses the set scratch_for(st) returns.
+constexpr int kScratchSets = 4;
+struct ScratchSet {
+  unsigned long long* scratch;
+  int32_t* counters;
+};
+ScratchSet scratch_for(hipStream_t st);
 extern int g_last_cfg;  // configuration of the last decode-regime launch (-2: prefill kernel)
 
 template <class Epi, int R, int LT, int WS, int WR, int U, bool XL, bool XS>
@@ -585,7 +588,7 @@ int run(Geometry g, const typename Epi::Out& o_in, hipStream_t st) {
     o.cand = nullptr;
     if (kind != 2 && g.nseg == 1) {
       nrb = (g.seg[0].row_tiles + rows_per_block - 1) / rows_per_block;
-      if (static_cast<int64_t>(nrb) * g.rows <= kCandSlots) o.cand = scratch_base();
+      if (static_cast<int64_t>(nrb) * g.rows <= kCandSlots) o.cand = scratch_for(st).scratch;
       if (!o.cand) nrb = 0;
       o.nrb = nrb;
     }
@@ -594,8 +597,9 @@ int run(Geometry g, const typename Epi::Out& o_in, hipStream_t st) {
     g_last_cfg = idx;
     const bool xs = kDecodeCfgs[idx].xs;
     if (xs) {
-      g.part = reinterpret_cast<float*>(scratch_base());
-      g.split_cnt = split_counters();
+      const ScratchSet ss = scratch_for(st);
+      g.part = reinterpret_cast<float*>(ss.scratch);
+      g.split_cnt = ss.counters;
       g.part_splits = smax;
       if (!g.part || !g.split_cnt) return fail(STRIDE_TC_EINVAL, "split scratch unavailable");
     }
@@ -603,8 +607,9 @@ int run(Geometry g, const typename Epi::Out& o_in, hipStream_t st) {
   } else if (kind == 3) {
     g_last_cfg = kDecIndexBase + idx;
     if (kDecCfgs[idx].xs) {
-      g.part = reinterpret_cast<float*>(scratch_base());
-      g.split_cnt = split_counters();
+      const ScratchSet ss = scratch_for(st);
+      g.part = reinterpret_cast<float*>(ss.scratch);
+      g.split_cnt = ss.counters;
       g.part_splits = smax;
       if (!g.part || !g.split_cnt) return fail(STRIDE_TC_EINVAL, "split scratch unavailable");
     }

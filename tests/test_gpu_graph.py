@@ -131,3 +131,45 @@ def test_engine_step_graph_replays_match_eager():
         eng.launch(len(rows), slot, pos, tok, items)  # eager work between replays (no LM head)
         torch.cuda.synchronize()
     del graph
+
+
+@pytest.mark.parametrize("m,cfg", [(1, 53), (64, -1), (64, 1007)])
+def test_two_streams_at_once(data, m, cfg):
+    """Launches that use the device scratch (cross-workgroup split partials and
+    counters, the greedy LM head's candidates) on two streams at the same time,
+    eight rounds each with no synchronisation in between: every stream gets the
+    results of its inputs run alone (each stream is given its own scratch set)."""
+    W, x, h = data
+    say("two streams M =", m, "config", cfg)
+    g = torch.Generator(device=DEV).manual_seed(m + 7)
+    xs = [x[2048][:m], (torch.randn(m, 2048, generator=g, device=DEV)).to(torch.bfloat16).view(torch.int16)]
+    xds = [x[8192][:m], (torch.randn(m, 8192, generator=g, device=DEV)).to(torch.bfloat16).view(torch.int16)]
+    sets = []
+    for xi, xdi in zip(xs, xds):
+        xt, xd = layout.lane_tiles(xi), layout.lane_tiles(xdi)
+        h_o0 = layout.lane_tiles(h[:m].clone())
+        h_d0 = layout.lane_tiles(h[:m, :512].clone())
+        best0 = harness.best_init(m, DEV)
+        z = torch.zeros(((m + 15) // 16, W["w1"].shape[0], 16, 16), dtype=torch.int16, device=DEV)
+        sets.append([xt, xd, h_o0, h_d0, torch.empty_like(h_o0), torch.empty_like(h_d0), torch.empty_like(best0),
+                     best0, z])
+    _lib.set_stream_config(cfg)
+    try:
+        refs = []
+        for xt, xd, h_o0, h_d0, h_o, h_d, best, best0, z in sets:
+            launch_set(W, xt, xd, h_o0, h_d0, h_o, h_d, best, best0, z, m)
+            torch.cuda.synchronize()
+            refs.append([digest(t) for t in (h_o, h_d, z, best)])
+        assert refs[0] != refs[1]
+        streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+        for s in streams:
+            s.wait_stream(torch.cuda.current_stream())
+        for _ in range(8):
+            for s, (xt, xd, h_o0, h_d0, h_o, h_d, best, best0, z) in zip(streams, sets):
+                with torch.cuda.stream(s):
+                    launch_set(W, xt, xd, h_o0, h_d0, h_o, h_d, best, best0, z, m)
+        torch.cuda.synchronize()
+        for ref, (xt, xd, h_o0, h_d0, h_o, h_d, best, best0, z) in zip(refs, sets):
+            assert [digest(t) for t in (h_o, h_d, z, best)] == ref
+    finally:
+        _lib.set_stream_config(-1)
