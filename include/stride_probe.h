@@ -47,6 +47,17 @@ int stride_probe_strip_read(const void* buf, int64_t bytes, int64_t strip, int32
 int stride_probe_mfma_equiv(const uint16_t* a, const uint16_t* b, const float* c0, float* o16, float* o32,
                             int32_t cases, int32_t chunks, void* stream);
 
+/* Decode-structure ceiling (measures the kernel structure, computes nothing
+ * useful): row_tiles / 4 workgroups of 4 compute waves, each streaming one
+ * weight strip of `chunks` 1 KiB chunks (a multiple of 16) from w into
+ * registers 16 chunks ahead and issuing lane_tiles (4 or 8) 16x16x32 bf16 MFMAs
+ * per chunk against activation fragments taken from registers (mode 0), from a
+ * static LDS slab with a barrier every 4 chunks (mode 1), or from an LDS ring
+ * that a fifth wave refills from x ([lane_tiles][chunks] 1 KiB chunks) with
+ * global_load_lds (mode 2, what a real kernel must do). out: row_tiles * 64 f32x4. */
+int stride_probe_decode_ceiling(const void* w, int32_t row_tiles, int32_t chunks, const void* x, int32_t lane_tiles,
+                                int32_t mode, float* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

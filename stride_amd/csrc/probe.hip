@@ -138,6 +138,87 @@ __global__ __launch_bounds__(256) void k_strip_read(const char* buf, int64_t nst
   if (x == 0x12345678u) out[0] = x;
 }
 
+
+// Decode-structure ceiling (measurement of the kernel structure, not a GEMM):
+// 4 compute waves per workgroup, one 16-row weight strip each (`chunks` 1 KiB
+// chunks streamed HBM -> registers, U = 16 ahead), LT lane tiles of activation
+// fragments per chunk, LT v_mfma_f32_16x16x32_bf16 per chunk. MODE 0: the
+// fragments are constants in registers; MODE 1: read from a static LDS slab,
+// one chunk ahead, with a barrier every 4 chunks; MODE 2: as 1 with a fifth
+// wave refilling the LDS ring (slabs of 4 chunks, 3 slots) from x
+// [LT][chunks] chunks by global_load_lds, as a real kernel must.
+template <int LT, int MODE>
+__global__ __launch_bounds__(320) void k_decode_ceiling(const u32x4* __restrict__ w, const u32x4* __restrict__ x,
+                                                         int chunks, f32x4* out) {
+  constexpr int U = 16, S = 4, NSLOT = 3, SLOT = S * LT * 64;
+  __shared__ u32x4 ring[NSLOT * SLOT];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nb = chunks / S;
+  if (wave == 4) {  // copy wave (MODE 2 only; otherwise it only keeps the barrier count)
+    auto issue = [&](int slab) {
+      if constexpr (MODE == 2) {
+        u32x4* dst = ring + (slab % NSLOT) * SLOT;
+#pragma unroll
+        for (int q = 0; q < S * LT; ++q) {
+          const int c = min(slab * S + q / LT, chunks - 1);
+          __builtin_amdgcn_global_load_lds(
+              (const __attribute__((address_space(1))) void*)(x + (static_cast<int64_t>(q % LT) * chunks + c) * 64 + lane),
+              (__attribute__((address_space(3))) void*)(dst + q * 64), 16, 0, 0);
+        }
+      }
+    };
+    for (int s = 0; s < NSLOT; ++s) issue(s);
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_s_barrier();
+    for (int j = 1; j <= nb; ++j) {
+      constexpr int n = (NSLOT - 2) * S * LT;
+      __builtin_amdgcn_s_waitcnt((n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+      __builtin_amdgcn_s_barrier();
+      issue(j + NSLOT - 1);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    return;
+  }
+  if (MODE != 2)
+    for (int i = threadIdx.x; i < NSLOT * SLOT; i += 256) ring[i] = u32x4{static_cast<uint32_t>(i) * 0x10001u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
+  const u32x4* wp = w + static_cast<int64_t>(blockIdx.x * 4 + wave) * chunks * 64 + lane;
+  f32x4 acc[LT];
+#pragma unroll
+  for (int l = 0; l < LT; ++l) acc[l] = f32x4{0.f, 0.f, 0.f, 0.f};
+  u32x4 buf[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) buf[u] = wp[static_cast<int64_t>(u) * 64];
+  u32x4 xf[2][LT];
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  __builtin_amdgcn_s_barrier();
+#pragma unroll
+  for (int l = 0; l < LT; ++l) xf[0][l] = MODE == 0 ? u32x4{0x3f803f80u, static_cast<uint32_t>(l), 0u, 0u} : ring[l * 64 + lane];
+  const int nbody = __builtin_amdgcn_readfirstlane(chunks / U);
+  for (int k = 0; k < nbody; ++k) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = k * U + u;
+      if ((u + 1) % S == 0) {
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+        __builtin_amdgcn_s_barrier();
+      }
+      const u32x4 a = buf[u];
+      buf[u] = wp[static_cast<int64_t>(min(c + U, chunks - 1)) * 64];
+      if constexpr (MODE != 0) {
+        const int cn = c + 1;
+#pragma unroll
+        for (int l = 0; l < LT; ++l) xf[(u + 1) & 1][l] = ring[((cn / S) % NSLOT) * SLOT + ((cn % S) * LT + l) * 64 + lane];
+      }
+#pragma unroll
+      for (int l = 0; l < LT; ++l) acc[l] = mfma(a, xf[MODE == 0 ? 0 : (u & 1)][l], acc[l]);
+    }
+  }
+  f32x4 r = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int l = 0; l < LT; ++l) r = r + acc[l];
+  out[(blockIdx.x * 4 + wave) * 64 + lane] = r;
+}
+
 }  // namespace
 
 extern "C" int stride_probe_mfma_rate_variant(float* out, int32_t blocks, int32_t iters, int32_t variant, void* stream) {
@@ -244,6 +325,28 @@ extern "C" int stride_probe_strip_read(const void* buf, int64_t bytes, int64_t s
     case 8: hipLaunchKernelGGL(k_strip_read<8>, dim3(blocks), dim3(256), 0, st, p, nstrips, strip, rotate, out); break;
     case 16: hipLaunchKernelGGL(k_strip_read<16>, dim3(blocks), dim3(256), 0, st, p, nstrips, strip, rotate, out); break;
     default: return 1;
+  }
+  return static_cast<int>(hipGetLastError());
+}
+
+extern "C" int stride_probe_decode_ceiling(const void* w, int32_t row_tiles, int32_t chunks, const void* x,
+                                           int32_t lane_tiles, int32_t mode, float* out, void* stream) {
+  if (!w || !out || row_tiles <= 0 || row_tiles % 4 != 0 || chunks <= 0 || chunks % 16 != 0 || mode < 0 || mode > 2 ||
+      (lane_tiles != 4 && lane_tiles != 8) || (mode == 2 && !x))
+    return 1;
+  const dim3 grid(row_tiles / 4), block(320);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const u32x4* wv = static_cast<const u32x4*>(w);
+  const u32x4* xv = static_cast<const u32x4*>(x);
+  f32x4* o = reinterpret_cast<f32x4*>(out);
+  if (lane_tiles == 8) {
+    if (mode == 0) hipLaunchKernelGGL((k_decode_ceiling<8, 0>), grid, block, 0, st, wv, xv, chunks, o);
+    else if (mode == 1) hipLaunchKernelGGL((k_decode_ceiling<8, 1>), grid, block, 0, st, wv, xv, chunks, o);
+    else hipLaunchKernelGGL((k_decode_ceiling<8, 2>), grid, block, 0, st, wv, xv, chunks, o);
+  } else {
+    if (mode == 0) hipLaunchKernelGGL((k_decode_ceiling<4, 0>), grid, block, 0, st, wv, xv, chunks, o);
+    else if (mode == 1) hipLaunchKernelGGL((k_decode_ceiling<4, 1>), grid, block, 0, st, wv, xv, chunks, o);
+    else hipLaunchKernelGGL((k_decode_ceiling<4, 2>), grid, block, 0, st, wv, xv, chunks, o);
   }
   return static_cast<int>(hipGetLastError());
 }

@@ -29,6 +29,8 @@ def load():
         lib.stride_probe_mfma_equiv.restype = C.c_int
         lib.stride_probe_strip_read.argtypes = [vp, C.c_int64, C.c_int64, C.c_int32, C.c_int32, C.c_int32, vp, vp]
         lib.stride_probe_strip_read.restype = C.c_int
+        lib.stride_probe_decode_ceiling.argtypes = [vp, C.c_int32, C.c_int32, vp, C.c_int32, C.c_int32, vp, vp]
+        lib.stride_probe_decode_ceiling.restype = C.c_int
         _lib = lib
     return _lib
 
@@ -72,6 +74,13 @@ def mfma_equiv(a, b, c0, o16, o32, chunks: int, stream: int) -> None:
         raise RuntimeError(f"stride_probe_mfma_equiv failed ({rc})")
 
 
+def decode_ceiling(w, row_tiles: int, chunks: int, x, lane_tiles: int, mode: int, out, stream: int) -> None:
+    rc = load().stride_probe_decode_ceiling(w.data_ptr(), row_tiles, chunks, x.data_ptr(), lane_tiles, mode,
+                                            out.data_ptr(), stream)
+    if rc:
+        raise RuntimeError(f"stride_probe_decode_ceiling failed ({rc})")
+
+
 def _graph_time(torch, fns, side):
     """Average seconds per call of fns (captured once in a HIP graph, replayed twice)."""
     g = torch.cuda.CUDAGraph()
@@ -95,7 +104,7 @@ def _graph_time(torch, fns, side):
 
 
 def main(argv=None) -> None:
-    """python -m stride_amd.probe [read] [strip] [mfma]: the floors the GEMM
+    """python -m stride_amd.probe [read] [strip] [mfma] [ceiling]: the floors the GEMM
     kernels are judged against, as markdown table rows. Buffers rotate over up to
     16 distinct copies in a 3 GiB pool, so the 256 MB MALL cannot serve repeats."""
     import sys
@@ -134,6 +143,21 @@ def main(argv=None) -> None:
                                for blocks in (256, 512, 1024) for unroll in (8, 16))
                     print(f"| {mib} MiB | {strip // 1024} KiB | {'yes' if rot else 'no'} | {best * 1e6:.2f} us | "
                           f"{nb / best / 1e9:.0f} |", flush=True)
+    if "ceiling" in what:
+        # The gate/up shape at M = 64 and 128: 1024 strips of 64 chunks (64 MiB),
+        # 16 copies rotated (1 GiB).
+        print("| lane tiles (M) | activation fragments | time | GB/s of weights |\n|---|---|---|---|", flush=True)
+        rt, ch = 1024, 64
+        nb = rt * ch * 1024
+        wpool = torch.empty(16 * nb, dtype=torch.uint8, device=dev).fill_(0x3c)
+        xb = torch.empty(8 * ch * 1024, dtype=torch.uint8, device=dev).fill_(0x3c)
+        fo = torch.zeros(rt * 64 * 4, dtype=torch.float32, device=dev)
+        views = [wpool[i * nb:(i + 1) * nb] for i in range(16)]
+        for lt in (4, 8):
+            for mode, label in ((0, "registers (no LDS)"), (1, "static LDS slab"), (2, "LDS ring refilled by a copy wave")):
+                s = _graph_time(torch, [lambda v=v: decode_ceiling(v, rt, ch, xb, lt, mode, fo, stream()) for v in views],
+                                side)
+                print(f"| {lt} ({16 * lt}) | {label} | {s * 1e6:.2f} us | {nb / s / 1e9:.0f} |", flush=True)
     if "mfma" in what:
         print("| form | waves per SIMD | TFLOP/s |\n|---|---|---|", flush=True)
         fo = torch.zeros(1 << 16, dtype=torch.float32, device=dev)
