@@ -271,7 +271,7 @@ int stride_tc_norm(const StrideTcNormParams* p, int per_lane, void* stream);
  * 93-103); then items and scratch are not read, the page records stay in LDS and
  * pages and combine run as one kernel (same bits). max_pages bounds the pages of
  * a row; max_pages * (12 + 4 * head_dim) floats plus the kernel's staging must
- * fit 159 KiB of LDS: up to 116 pages (7424 positions) at head_dim 64, 43 at
+ * fit 159 KiB of LDS: up to 117 pages (7488 positions) at head_dim 64, 44 at
  * head_dim 128; larger values are rejected (use an item list). */
 int stride_tc_attention(const StrideAttentionParams* p, void* stream);
 

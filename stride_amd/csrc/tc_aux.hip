@@ -366,10 +366,8 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_fused(StrideAttentionParams p
   constexpr int kKey = D / kEl;                 // 16-byte pieces of one K row
   constexpr int RF = 8 + kHeadsPerGroup * D;    // record floats
   extern __shared__ float recs[];               // [pages][RF], then f[4][pages]
-  __shared__ f32x4 q4[D];
   __shared__ f32x4 w4[NWV][kAttnPage];
   __shared__ uint16_t vs[NWV][kAttnPage][D];
-  __shared__ float den[kHeadsPerGroup];
   const int j = blockIdx.x / p.n_kv;
   const int g = blockIdx.x % p.n_kv;
   const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
@@ -378,32 +376,42 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_fused(StrideAttentionParams p
   const int last = visible - 1;
   const int pages = (last >> kAttnPageShift) + 1;
   const float* qrow = p.q + static_cast<int64_t>(j) * p.q_stride + static_cast<int64_t>(g * kHeadsPerGroup) * D;
-  for (int d = t; d < D; d += 64 * NWV) q4[d] = f32x4{qrow[d], qrow[D + d], qrow[2 * D + d], qrow[3 * D + d]};
+  // The query row is the same for every lane: read through the scalar cache into
+  // SGPRs, so the scores take their query operands without LDS reads.
+  typedef const __attribute__((address_space(4))) float ConstF;
+  ConstF* cq = (ConstF*)(qrow);
   const float neg_inf = f32_of(0xFF800000u);
   const int rounds = (pages + NWV - 1) / NWV;  // the same for every wave: barriers stay uniform
+  // K and V of the wave's next page are loaded into registers one round ahead:
+  // they stream in while the current page is scored and mixed.
+  u32x4 vr[kPer], kr[kKey];
+  auto fetch = [&](int page) {
+    const int p0 = page << kAttnPageShift;
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int P = k * 64 + lane, i = P / (D / kEl), c = P % (D / kEl);
+      vr[k] = load16(kv_row<uint16_t>(p.kv, page_shift, p.layer, 1, g, slot, min(p0 + i, last)) + c * kEl);
+    }
+    const uint16_t* key = kv_row<uint16_t>(p.kv, page_shift, p.layer, 0, g, slot, min(p0 + lane, last));
+#pragma unroll
+    for (int c = 0; c < kKey; ++c) kr[c] = load16(key + kEl * c);
+  };
+  if (wave < pages) fetch(wave);
   for (int it = 0; it < rounds; ++it) {
     const int page = it * NWV + wave;
     const bool active = page < pages;
     const int p0 = page << kAttnPageShift;
     const int n = active ? min(visible - p0, kAttnPage) : 0;
-    u32x4 vr[kPer], kr[kKey];
     if (active) {
-#pragma unroll
-      for (int k = 0; k < kPer; ++k) {
-        const int P = k * 64 + lane, i = P / (D / kEl), c = P % (D / kEl);
-        vr[k] = load16(kv_row<uint16_t>(p.kv, page_shift, p.layer, 1, g, slot, min(p0 + i, last)) + c * kEl);
-      }
-      const uint16_t* key = kv_row<uint16_t>(p.kv, page_shift, p.layer, 0, g, slot, min(p0 + lane, last));
-#pragma unroll
-      for (int c = 0; c < kKey; ++c) kr[c] = load16(key + kEl * c);
 #pragma unroll
       for (int k = 0; k < kPer; ++k) {
         const int P = k * 64 + lane;
         *reinterpret_cast<u32x4*>(&vs[wave][P / (D / kEl)][(P % (D / kEl)) * kEl]) = vr[k];
       }
     }
-    __syncthreads();  // q4 (first round) and this wave's V rows
+    __syncthreads();  // this wave's V rows
     f32x4 mx = {0.f, 0.f, 0.f, 0.f};
+    float sc[kHeadsPerGroup] = {0.f, 0.f, 0.f, 0.f};
     if (active) {
       float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
 #pragma unroll
@@ -411,7 +419,8 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_fused(StrideAttentionParams p
 #pragma unroll
         for (int e = 0; e < kEl; ++e) {
           const float k = f32_of(e & 1 ? kr[c][e >> 1] & 0xFFFF0000u : kr[c][e >> 1] << 16);
-          const f32x4 qd = q4[kEl * c + e];
+          const int d = kEl * c + e;
+          const f32x4 qd = f32x4{cq[d], cq[D + d], cq[2 * D + d], cq[3 * D + d]};
           a0 = __builtin_fmaf(qd[0], k, a0);
           a1 = __builtin_fmaf(qd[1], k, a1);
           a2 = __builtin_fmaf(qd[2], k, a2);
@@ -419,7 +428,13 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_fused(StrideAttentionParams p
         }
         __builtin_amdgcn_sched_barrier(0);
       }
-      float sc[kHeadsPerGroup] = {a0 * p.scale, a1 * p.scale, a2 * p.scale, a3 * p.scale};
+      sc[0] = a0 * p.scale;
+      sc[1] = a1 * p.scale;
+      sc[2] = a2 * p.scale;
+      sc[3] = a3 * p.scale;
+    }
+    if (page + NWV < pages) fetch(page + NWV);  // registers are free again
+    if (active) {
 #pragma unroll
       for (int h = 0; h < kHeadsPerGroup; ++h) {
         if (lane >= n) sc[h] = neg_inf;
@@ -462,21 +477,19 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_fused(StrideAttentionParams p
     }
     __syncthreads();  // the staging buffers are reused by the next round
   }
-  // Combine in ascending page order (k_attn_combine's expressions).
+  // Combine in ascending page order (k_attn_combine's expressions). Each page
+  // factor is computed by its own thread; every thread derives the head maximum
+  // with the same ascending loop, so all agree; each output thread then forms
+  // its head's denominator and its dim's sum over the pages in order.
   float* f = recs + pages * RF;
-  if (t < kHeadsPerGroup) {
+  for (int u = t; u < kHeadsPerGroup * pages; u += 64 * NWV) {
+    const int h = u & 3, c = u >> 2;
     float m = neg_inf;
-    for (int c = 0; c < pages; ++c) {
-      const float mc = recs[c * RF + t];
+    for (int c2 = 0; c2 < pages; ++c2) {
+      const float mc = recs[c2 * RF + h];
       if (mc > m) m = mc;
     }
-    float d = 0.0f;
-    for (int c = 0; c < pages; ++c) {
-      const float e = det_exp(recs[c * RF + t] - m);
-      f[t * pages + c] = e;
-      d = __builtin_fmaf(e, recs[c * RF + 4 + t], d);
-    }
-    den[t] = d;
+    f[h * pages + c] = det_exp(recs[c * RF + h] - m);
   }
   __syncthreads();
   const int col_tiles = p.out_cols >> 4;
@@ -484,10 +497,14 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_fused(StrideAttentionParams p
   const int64_t lane0 = static_cast<int64_t>(j >> 4) * col_tiles * kTileElems + (j & 15) * 16;
   for (int hd = t; hd < kHeadsPerGroup * D; hd += 64 * NWV) {
     const int qh = hd / D, d = hd % D;
-    float acc = 0.0f;
-    for (int c = 0; c < pages; ++c) acc = __builtin_fmaf(f[qh * pages + c], recs[c * RF + 8 + qh * D + d], acc);
+    float acc = 0.0f, dn = 0.0f;
+    for (int c = 0; c < pages; ++c) {
+      const float e = f[qh * pages + c];
+      dn = __builtin_fmaf(e, recs[c * RF + 4 + qh], dn);
+      acc = __builtin_fmaf(e, recs[c * RF + 8 + qh * D + d], acc);
+    }
     const int idx = (g * kHeadsPerGroup + qh) * D + d;
-    out[lane0 + static_cast<int64_t>(idx >> 4) * kTileElems + (idx & 15)] = static_cast<uint16_t>(bf16_rne(acc / den[qh]));
+    out[lane0 + static_cast<int64_t>(idx >> 4) * kTileElems + (idx & 15)] = static_cast<uint16_t>(bf16_rne(acc / dn));
   }
 }
 
@@ -524,11 +541,11 @@ static int combine(dim3 grid, size_t lds, hipStream_t st, const StrideAttentionP
   return launched("attention (combine)");
 }
 
-// One-kernel attention (item_count == -1); its static LDS (staging for four
-// waves) and the row's records share the 160 KiB.
+// One-kernel attention (item_count == -1); its static LDS (staging for up to
+// four waves) and the row's records share the 160 KiB.
 template <int D, int NWV>
 static int fused_nwv(dim3 grid, size_t lds, hipStream_t st, const StrideAttentionParams& p, int page_shift) {
-  constexpr size_t kStatic = D * 16 + NWV * 64 * 16 + NWV * 64 * D * 2 + 64;
+  constexpr size_t kStatic = NWV * 64 * 16 + NWV * 64 * D * 2;
   if (lds + kStatic > kCombineLdsMax)
     return fail(STRIDE_TC_EINVAL, "tc_attention: max_pages too large for the one-kernel form (use an item list)");
   static size_t raised = 64 * 1024;
@@ -544,8 +561,9 @@ static int fused_nwv(dim3 grid, size_t lds, hipStream_t st, const StrideAttentio
 
 // Waves per workgroup of the one-kernel form, from measurements of the full
 // decode step at position 383 (six pages per row): with many (row, group)
-// workgroups (batch 128, 1024 of them) two waves per workgroup keep more
-// workgroups resident; with fewer (batch 64) four waves finish a row sooner.
+// workgroups (batch 128, 1024 of them) two waves per workgroup (three rounds of
+// pages) measured best (30.9 us against 32.4 with three and 33+ with four); with
+// fewer (batch 64) four waves finish a row sooner.
 template <int D>
 static int fused(dim3 grid, size_t lds, hipStream_t st, const StrideAttentionParams& p, int page_shift) {
   if (grid.x >= 768) return fused_nwv<D, 2>(grid, lds, st, p, page_shift);
