@@ -351,12 +351,25 @@ template <class Epi, int WRT, int WLT, int WM, int WN, int KC, int NS, int OCC, 
 void launch_pipe(Geometry g, const typename Epi::Out& o, int smax, hipStream_t st) {
   constexpr int BR = WM * WRT, BL = WN * WLT;
   int blocks = 0;
-  for (int i = 0; i < g.nseg; ++i) {
-    g.seg[i].blocks = (g.seg[i].row_tiles + BR - 1) / BR;
-    blocks += g.seg[i].blocks;
+  if constexpr (MF32 == 2) {  // FLAT: one range of row tiles over all segments
+    int total = 0;
+    for (int i = 0; i < g.nseg; ++i) total += g.seg[i].row_tiles;
+    for (int i = g.nseg; i < 3; ++i) g.seg[i].row_tiles = 0;
+    for (int i = 1; i < 3; ++i) g.seg[i].blocks = 0;
+    g.seg[0].blocks = blocks = (total + BR - 1) / BR;
+  } else {
+    for (int i = 0; i < g.nseg; ++i) {
+      g.seg[i].blocks = (g.seg[i].row_tiles + BR - 1) / BR;
+      blocks += g.seg[i].blocks;
+    }
   }
   blocks *= (g.lane_groups + BL - 1) / BL;
-  if constexpr (MF32) {
+  if constexpr (MF32 == 2) {
+    if (smax > 1)
+      hipLaunchKernelGGL((k_pipe<Epi, WRT, WLT, WM, WN, KC, NS, OCC, true, true>), dim3(blocks), dim3(kWave * WM * WN), 0, st, g, o);
+    else
+      hipLaunchKernelGGL((k_pipe<Epi, WRT, WLT, WM, WN, KC, NS, OCC, false, true>), dim3(blocks), dim3(kWave * WM * WN), 0, st, g, o);
+  } else if constexpr (MF32) {
     if (smax > 1)
       hipLaunchKernelGGL((k_pipe32<Epi, WRT, WLT, WM, WN, KC, NS, OCC, true>), dim3(blocks), dim3(kWave * WM * WN), 0, st, g, o);
     else
@@ -371,7 +384,8 @@ void launch_pipe(Geometry g, const typename Epi::Out& o, int smax, hipStream_t s
 
 // Prefill configurations of k_pipe: (WRT, WLT, WM, WN, KC, NS, OCC, MF32). For
 // the paired gate/up GEMM WRT counts pairs and is halved (two matrices per row
-// tile). MF32 = 1 runs k_pipe32 (32x32x16 MFMAs; same bits).
+// tile). MF32 = 1 runs k_pipe32 (32x32x16 MFMAs; same bits); MF32 = 2 runs
+// k_pipe with FLAT row blocks (blocks may straddle QKV segments; same bits).
 // Index -3 - i in the tuning hook selects configuration i.
 #define STRIDE_TC_PIPE_CONFIGS(X) \
   X(0, 4, 4, 2, 2, 2, 3, 1, 0) \
@@ -405,9 +419,11 @@ void launch_pipe(Geometry g, const typename Epi::Out& o, int smax, hipStream_t s
   X(28, 4, 4, 2, 4, 2, 3, 1, 0) \
   X(29, 4, 4, 2, 4, 1, 4, 1, 0) \
   X(30, 4, 4, 2, 4, 1, 6, 1, 0) \
-  X(31, 4, 8, 2, 2, 1, 4, 1, 0)
+  X(31, 4, 8, 2, 2, 1, 4, 1, 0) \
+  X(32, 3, 4, 4, 2, 2, 3, 1, 2) \
+  X(33, 6, 2, 2, 4, 2, 3, 1, 2)
 
-constexpr int kNumPipeCfgs = 32;
+constexpr int kNumPipeCfgs = 34;
 extern int g_forced_pipe;
 
 template <class Epi>
@@ -442,7 +458,15 @@ inline bool pipe_cfg_fits(int idx, const Geometry& g) {
       STRIDE_TC_PIPE_CONFIGS(STRIDE_TC_PIPE_KC)
 #undef STRIDE_TC_PIPE_KC
   };
+  static const int mf[] = {
+#define STRIDE_TC_PIPE_MF(i, WRT, WLT, WM, WN, KC, NS, OCC, MF) MF,
+      STRIDE_TC_PIPE_CONFIGS(STRIDE_TC_PIPE_MF)
+#undef STRIDE_TC_PIPE_MF
+  };
   if (g.col_tiles & 1) return false;  // whole 32-column chunks only
+  if (mf[idx] == 2)  // FLAT blocks: one split count for every segment
+    for (int i = 1; i < g.nseg; ++i)
+      if (g.seg[i].splits != g.seg[0].splits) return false;
   const int chunks = g.col_tiles >> 1;
   // An odd chunk count per stage is processed two stages at a time.
   const int step = kc[idx] % 2 ? 2 * kc[idx] : kc[idx];
@@ -512,8 +536,10 @@ inline Pick pick_large(const Geometry& g, int T, int smax, int per) {
     if (T <= 12) return {0, 33};
     if (T <= 24) return {0, 29};
     if (T <= 64) return {1, 14};
-    if (T <= 128) return {1, 28};
-    return {1, 26};
+    // 12-row-tile blocks straddling the q/k/v segments: the 192 row tiles make
+    // 16 row blocks, 256 workgroups at M = 2048 (the segment-aligned blocks give
+    // 192 or 384): 39.0 against 46.5 us at M = 2048, 76.9 against 89.5 at 4096.
+    return {1, 33};
   }
   if (per >= 32) {  // long splits (down)
     if (T <= 12 && dec_cfg_fits(kDecCfgs[7], g, smax, 1, false)) return {3, 7};  // one split per workgroup

@@ -38,7 +38,27 @@ constexpr int vm_lgkm0_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 <
 // lgkmcnt = 0 only (vmcnt and expcnt at their no-wait maxima).
 constexpr int lgkm0_imm() { return vmcnt_imm(63) & ~(0xF << 8); }
 
-template <class Epi, int WRT, int WLT, int WM, int WN, int KC, int NS, int OCC, bool HASY>
+// Row tile rt of the segments laid end to end: its segment, and its index there.
+__device__ __forceinline__ int flat_segment(const Geometry& g, int rt, int& local) {
+  const int r0 = g.seg[0].row_tiles, r1 = g.seg[1].row_tiles;
+  if (rt < r0) {
+    local = rt;
+    return 0;
+  }
+  if (rt < r0 + r1) {
+    local = rt - r0;
+    return 1;
+  }
+  local = rt - r0 - r1;
+  return 2;
+}
+
+// FLAT: the segments' row tiles form one range (they share the split count), so
+// a block may straddle two segments; each row tile reads its own segment's
+// weights and goes to its own segment's epilogue. This lets the block height be
+// chosen for the grid size (e.g. 12 row tiles: the fused QKV's 192 row tiles in
+// 16 blocks) rather than for the segment sizes.
+template <class Epi, int WRT, int WLT, int WM, int WN, int KC, int NS, int OCC, bool HASY, bool FLAT = false>
 __global__ __launch_bounds__(kWave * WM * WN, OCC) void k_pipe(Geometry g, typename Epi::Out o) {
   constexpr int M = Epi::kMats;
   constexpr int NW = WM * WN;
@@ -58,8 +78,11 @@ __global__ __launch_bounds__(kWave * WM * WN, OCC) void k_pipe(Geometry g, typen
   // lane blocks together so that consecutive workgroups (which the hardware puts
   // on one XCD after xcd_remap) share activation tiles in L2.
   int b = xcd_remap(blockIdx.x, gridDim.x);
-  const int si = locate_segment(g, b, lblocks);
+  const int si = FLAT ? 0 : locate_segment(g, b, lblocks);
   const Segment sg = seg_at(g, si);
+  // Row tiles of this block's range (FLAT: all segments; the host sets
+  // seg[0].blocks to the row blocks of the whole range).
+  const int total = FLAT ? g.seg[0].row_tiles + g.seg[1].row_tiles + g.seg[2].row_tiles : sg.row_tiles;
   constexpr int G = 8;
   const int group = b / (G * lblocks);
   const int gsize = min(G, sg.blocks - group * G);
@@ -83,8 +106,14 @@ __global__ __launch_bounds__(kWave * WM * WN, OCC) void k_pipe(Geometry g, typen
     const uint16_t* base;
     if (blk < M * BR) {
       const int m = blk / BR;
-      const int rt = min(rt0 + blk % BR, sg.row_tiles - 1);
-      base = (m == 0 ? sg.w[0] : sg.w[1]) + rt * strip;  // no run-time index into sg
+      const int rt = min(rt0 + blk % BR, total - 1);
+      if constexpr (FLAT) {
+        int local = 0;
+        const Segment ss = seg_at(g, flat_segment(g, rt, local));
+        base = (m == 0 ? ss.w[0] : ss.w[1]) + local * strip;
+      } else {
+        base = (m == 0 ? sg.w[0] : sg.w[1]) + rt * strip;  // no run-time index into sg
+      }
     } else {
       const int lt = min(lt0 + blk - M * BR, g.lane_groups - 1);
       base = g.x + lt * strip;
@@ -182,7 +211,9 @@ __global__ __launch_bounds__(kWave * WM * WN, OCC) void k_pipe(Geometry g, typen
           acc[m][r][l] = f32x4{0.f, 0.f, 0.f, 0.f};
           if constexpr (Epi::kInitFromOutput) {
             const int rt = rt0 + wr * WRT + r, lt = lt0 + wn * WLT + l;
-            if (s == 0 && rt < sg.row_tiles && lt < g.lane_groups) acc[m][r][l] = Epi::init(o, rt, lt, lane);
+            int local = rt;
+            if constexpr (FLAT) flat_segment(g, rt, local);
+            if (s == 0 && rt < total && lt < g.lane_groups) acc[m][r][l] = Epi::init(o, local, lt, lane);
           }
         }
     if constexpr (kPairStages) {
@@ -215,9 +246,11 @@ __global__ __launch_bounds__(kWave * WM * WN, OCC) void k_pipe(Geometry g, typen
 #pragma unroll
       for (int r = 0; r < WRT; ++r) {
         const int rt = rt0 + wr * WRT + r;
-        if (rt >= sg.row_tiles) continue;
-        if constexpr (HASY) Epi::merge_tile(o, rt, y[0][r][l], lane, bv, bi);
-        else Epi::merge_tile(o, rt, acc[0][r][l], lane, bv, bi);
+        if (rt >= total) continue;
+        int local = rt;
+        if constexpr (FLAT) flat_segment(g, rt, local);
+        if constexpr (HASY) Epi::merge_tile(o, local, y[0][r][l], lane, bv, bi);
+        else Epi::merge_tile(o, local, acc[0][r][l], lane, bv, bi);
       }
       if (lane < 16) {
         cand_v[(wr * BL + wn * WLT + l) * 16 + lane] = bv;
@@ -242,7 +275,9 @@ __global__ __launch_bounds__(kWave * WM * WN, OCC) void k_pipe(Geometry g, typen
   }
   unroll<WRT>([&](auto r) {
     const int rt = rt0 + wr * WRT + r;
-    if (rt >= sg.row_tiles) return;
+    if (rt >= total) return;
+    int local = rt, seg = si;
+    if constexpr (FLAT) seg = flat_segment(g, rt, local);
     unroll<WLT>([&](auto l) {
       const int lt = lt0 + wn * WLT + l;
       if (lt >= g.lane_groups) return;
@@ -252,7 +287,7 @@ __global__ __launch_bounds__(kWave * WM * WN, OCC) void k_pipe(Geometry g, typen
         if constexpr (HASY) t[m] = y[m][r][l];
         else t[m] = acc[m][r][l];
       }
-      Epi::apply(o, g, si, rt, lt, t, lane);
+      Epi::apply(o, g, seg, local, lt, t, lane);
     });
   });
 }
