@@ -449,6 +449,13 @@ def main():
     if a.engine_only:
         print(json.dumps({"full_decode_step": engine_step(torch, dev, a.m, a.steps, a.warmup)}), flush=True)
         return
+    if a.copy_calib_mib:
+        src = torch.ones(a.copy_calib_mib << 18, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        torch.neg(src, out=dst)  # a plain streaming kernel: reads and writes exactly N bytes
+        torch.cuda.synchronize()
+        del src, dst
+
     model = Model(torch, dev)
     b = Buffers(torch, dev, a.m)
     ops = step_ops(model, b)
@@ -462,13 +469,6 @@ def main():
         print(json.dumps({"op": a.op, "M": a.m, "us": round(sec * 1e6, 2), "spread_us": [round(lo * 1e6, 2), round(hi * 1e6, 2)],
                           "GB/s": round(byt / sec / 1e9, 1), "TFLOP/s": round(f / sec / 1e12, 1)}), flush=True)
         return
-
-    if a.copy_calib_mib:
-        src = torch.ones(a.copy_calib_mib << 18, dtype=torch.float32, device=dev)
-        dst = torch.empty_like(src)
-        torch.neg(src, out=dst)  # a plain streaming kernel: reads and writes exactly N bytes
-        torch.cuda.synchronize()
-        del src, dst
 
     from stride_amd import harness
 
