@@ -270,9 +270,10 @@ int stride_tc_norm(const StrideTcNormParams* p, int per_lane, void* stream);
  * every row, the list the reference's engine always builds (src/engine.cpp:
  * 93-103); then items and scratch are not read, the page records stay in LDS and
  * pages and combine run as one kernel (same bits). max_pages bounds the pages of
- * a row; max_pages * (12 + 4 * head_dim) floats plus the kernel's staging must
- * fit 159 KiB of LDS: up to 117 pages (7488 positions) at head_dim 64, 44 at
- * head_dim 128; larger values are rejected (use an item list). */
+ * a row; max_pages * (12 + 4 * head_dim) floats, the row's KV page numbers
+ * (4 bytes each) and the kernel's staging must fit 159 KiB of LDS: with 16-token
+ * KV pages up to 115 pages (7360 positions) at head_dim 64, 44 at head_dim 128;
+ * larger values are rejected (use an item list). */
 int stride_tc_attention(const StrideAttentionParams* p, void* stream);
 
 /* Replaces stride::tc_compact (src/kernels_tc.h:85, src/kernels_tc.cu:566-587):

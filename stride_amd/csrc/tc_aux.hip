@@ -365,7 +365,7 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_fused(StrideAttentionParams p
   constexpr int kPer = kAttnPage * D / kEl / 64;  // V pieces per lane
   constexpr int kKey = D / kEl;                 // 16-byte pieces of one K row
   constexpr int RF = 8 + kHeadsPerGroup * D;    // record floats
-  extern __shared__ float recs[];               // [pages][RF], then f[4][pages]
+  extern __shared__ float recs[];  // [max_pages][RF], f[4][max_pages], then the row's KV page numbers
   __shared__ f32x4 w4[NWV][kAttnPage];
   __shared__ uint16_t vs[NWV][kAttnPage][D];
   const int j = blockIdx.x / p.n_kv;
@@ -375,6 +375,17 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_fused(StrideAttentionParams p
   const int visible = p.row_pos[j] + 1;
   const int last = visible - 1;
   const int pages = (last >> kAttnPageShift) + 1;
+  // The row's KV page numbers, read once: every K/V address below then comes
+  // from LDS, so a page's loads never wait on a dependent page-table load.
+  int32_t* btab = reinterpret_cast<int32_t*>(recs + p.max_pages * (RF + kHeadsPerGroup));
+  const int nblk = (last >> page_shift) + 1;
+  for (int i = t; i < nblk; i += 64 * NWV) btab[i] = p.kv.table[static_cast<int64_t>(slot) * p.kv.max_blocks + i];
+  const uint16_t* kv_base = static_cast<const uint16_t*>(p.kv.arena) + p.layer * p.kv.layer_elems + g * p.kv.group_elems;
+  auto kv_at = [&](int which, int pos) {
+    return kv_base + btab[pos >> page_shift] * p.kv.block_elems + which * p.kv.which_elems +
+           static_cast<int64_t>(pos & ((1 << page_shift) - 1)) * D;
+  };
+  __syncthreads();
   const float* qrow = p.q + static_cast<int64_t>(j) * p.q_stride + static_cast<int64_t>(g * kHeadsPerGroup) * D;
   // The query row is the same for every lane: read through the scalar cache into
   // SGPRs, so the scores take their query operands without LDS reads.
@@ -390,9 +401,9 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_fused(StrideAttentionParams p
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
       const int P = k * 64 + lane, i = P / (D / kEl), c = P % (D / kEl);
-      vr[k] = load16(kv_row<uint16_t>(p.kv, page_shift, p.layer, 1, g, slot, min(p0 + i, last)) + c * kEl);
+      vr[k] = load16(kv_at(1, min(p0 + i, last)) + c * kEl);
     }
-    const uint16_t* key = kv_row<uint16_t>(p.kv, page_shift, p.layer, 0, g, slot, min(p0 + lane, last));
+    const uint16_t* key = kv_at(0, min(p0 + lane, last));
 #pragma unroll
     for (int c = 0; c < kKey; ++c) kr[c] = load16(key + kEl * c);
   };
@@ -642,7 +653,9 @@ static int attention(const StrideAttentionParams* p, void* stream, const char* n
   hipStream_t st = static_cast<hipStream_t>(stream);
   if constexpr (!kExact) {
     if (p->item_count == -1) {
-      const size_t lds = static_cast<size_t>(p->max_pages) * (8 + 4 * D + kHeadsPerGroup) * sizeof(float);
+      // records and page factors, then the row's KV page numbers
+      const size_t blocks = (static_cast<size_t>(p->max_pages) * kAttnPage + page_tokens - 1) / page_tokens;
+      const size_t lds = static_cast<size_t>(p->max_pages) * (8 + 4 * D + kHeadsPerGroup) * sizeof(float) + blocks * 4;
       const dim3 grid(p->l.rows * p->n_kv);
       if (D == 32) return fused<32>(grid, lds, st, *p, page_shift);
       if (D == 64) return fused<64>(grid, lds, st, *p, page_shift);

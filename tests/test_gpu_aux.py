@@ -97,7 +97,7 @@ def test_compact():
 
 @pytest.mark.parametrize("page_tokens,n_kv,hd,cap,m", [(16, 8, 64, 320, 21), (64, 8, 64, 320, 21),
                                                         (16, 2, 128, 2048, 3), (32, 1, 32, 200, 9),
-                                                        (16, 8, 64, 512, 130), (16, 1, 64, 7488, 2),
+                                                        (16, 8, 64, 512, 130), (16, 1, 64, 7360, 2),
                                                         (16, 1, 128, 2816, 2)])
 def test_attention(exact, page_tokens, n_kv, hd, cap, m):
     say("tc_attention page_tokens", page_tokens, "n_kv", n_kv, "hd", hd, "cap", cap, "m", m)
