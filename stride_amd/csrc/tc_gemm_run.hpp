@@ -31,11 +31,14 @@ int fail(int code, const std::string& msg);
 
 // The fixed K-split for an N x K weight matrix. Matrices with few row tiles
 // (N <= 4096: Q, K, V, output, down) get 8 splits so that a decode launch has
-// enough independent weight streams; gate/up (N <= 16384) get 2; the LM head
-// gets 1. S is then capped by the chunk count and halved until it divides it.
+// enough independent weight streams; larger ones (gate and up at N = 8192, the
+// LM head) get 1: they have row tiles enough for the decode launches, and a
+// single split lets the prefill kernels keep one accumulator per tile instead
+// of a split partial and a running sum. S is then capped by the chunk count and
+// halved until it divides it.
 inline int split_count(int n, int k) {
   const int chunks = k / kChunkCols;
-  int s = n <= 4096 ? 8 : (n <= 16384 ? 2 : 1);
+  int s = n <= 4096 ? 8 : 1;
   if (s > chunks) s = chunks;
   while (s > 1 && chunks % s != 0) s >>= 1;
   return s < 1 ? 1 : s;
@@ -509,6 +512,11 @@ struct Pick {
 // two to four (one split per workgroup); otherwise the LDS-pipelined kernel with
 // small blocks wins for the LM head and for gate/up from five lane tiles.
 inline Pick pick_small(int T, int smax, int mats, int nseg, int per) {
+  if (smax == 1 && mats == 2) {  // gate/up (single split): 14.2 / 15.1 / 15.4 / 20.6 us at M = 1 / 32 / 64 / 128
+    if (T <= 1) return {0, 34};
+    if (T <= 4) return {1, 14};
+    return {3, 10};
+  }
   if (smax == 1 && T <= 2) return {3, 10};
   if (smax == 1 && T >= 3 && T <= 4) return {3, 8};
   if (smax == 1 && T == 8) return {3, 12};
@@ -523,7 +531,14 @@ inline Pick pick_small(int T, int smax, int mats, int nseg, int per) {
 // tiles and long split chains: up to a few hundred rows the streaming kernel,
 // whose waves run the splits side by side, beats the pipeline, which walks them
 // one after another; beyond, the pipeline with a block shape per size.
-inline Pick pick_large(const Geometry& g, int T, int smax, int per) {
+inline Pick pick_large(const Geometry& g, int T, int smax, int mats, int per) {
+  if (smax == 1 && mats == 2) {  // gate/up (single split)
+    if (T <= 16) return {3, 4};   // 25.1-25.5 us at M = 160-256
+    if (T <= 20) return {1, 30};  // 35.5 us at M = 290
+    if (T <= 24) return {1, 26};
+    if (T <= 40) return {1, 23};  // 40.2 us at M = 512
+    return {1, 4};                // 256 x 256 blocks: 63.0 / 122.5 / 233.4 us at M = 1024 / 2048 / 4096
+  }
   if (smax == 1) return {1, T <= 12 ? 3 : (T <= 24 ? 8 : 6)};
   if (smax == 2) {
     if (T <= 12) return {1, 12};
@@ -582,7 +597,7 @@ int run(Geometry g, const typename Epi::Out& o_in, hipStream_t st) {
     kind = 1;
     idx = g_forced_pipe;
   } else {
-    const Pick p = T <= kStreamMaxLaneTiles ? pick_small(T, smax, Epi::kMats, g.nseg, per) : pick_large(g, T, smax, per);
+    const Pick p = T <= kStreamMaxLaneTiles ? pick_small(T, smax, Epi::kMats, g.nseg, per) : pick_large(g, T, smax, Epi::kMats, per);
     kind = p.kind;
     idx = p.idx;
     if (g.col_tiles & 1) {
