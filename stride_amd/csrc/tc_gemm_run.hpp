@@ -250,7 +250,8 @@ inline bool decode_cfg_fits(const DecodeCfg& c, Geometry g, int smax, int mats, 
   D(18, 2, 4, 4, 2, 4, false, 1, 2)   \
   D(19, 4, 4, 4, 1, 4, false, 1, 2)   \
   D(20, 1, 8, 4, 1, 4, false, 2, 2)   \
-  D(21, 2, 8, 8, 1, 4, false, 1, 1)
+  D(21, 2, 8, 8, 1, 4, false, 1, 1)   \
+  D(22, 1, 10, 4, 2, 4, false, 1, 1)
 
 struct DecCfg {
   int r, lt, nw, kc, nss;
@@ -534,12 +535,17 @@ inline Pick pick_small(int T, int smax, int mats, int nseg, int per) {
 inline Pick pick_large(const Geometry& g, int T, int smax, int mats, int per) {
   if (smax == 1 && mats == 2) {  // gate/up (single split)
     if (T <= 16) return {3, 4};   // 25.1-25.5 us at M = 160-256
-    if (T <= 20) return {1, 30};  // 35.5 us at M = 290
+    if (T <= 20) return {3, 22};  // ten lane tiles per workgroup: 30.7 us at M = 290 (pipeline: 35.5)
     if (T <= 24) return {1, 26};
     if (T <= 40) return {1, 23};  // 40.2 us at M = 512
     return {1, 4};                // 256 x 256 blocks: 63.0 / 122.5 / 233.4 us at M = 1024 / 2048 / 4096
   }
-  if (smax == 1) return {1, T <= 12 ? 3 : (T <= 24 ? 8 : 6)};
+  if (smax == 1) {  // LM head: weights to registers at 9-12 and 17-24 lane tiles (M = 160 / 290 / 384:
+                    // 150 / 205 / 226 us against 186 / 269 / 263 with the pipeline), 256 x 256 blocks otherwise
+    if (T <= 12 || (T > 16 && T <= 20)) return {3, 19};
+    if (T > 20 && T <= 24) return {3, 14};
+    return {1, 6};
+  }
   if (smax == 2) {
     if (T <= 12) return {1, 12};
     if (T <= 24) return {1, 8};
