@@ -29,7 +29,7 @@ def setup():
     def w(n, k, rows=None):
         return layout.pack_tiles((torch.randn(n, k, generator=g, device=DEV) * 0.02).to(torch.bfloat16).view(torch.int16), rows)
 
-    W = dict(o=w(2048, 2048), down=w(512, 8192), w1=w(1024, 2048), w3=w(1024, 2048), lm=w(4000, 2048), lm1=w(16400, 2048),
+    W = dict(o=w(2048, 2048), down=w(512, 8192), w1=w(1024, 2048), w3=w(1024, 2048), w1b=w(8192, 2048), w3b=w(8192, 2048), lm=w(4000, 2048), lm1=w(16400, 2048),
              q=w(512, 2048, layout.rope_rows(512, 64)), k=w(128, 2048, layout.rope_rows(128, 64)),
              v=w(128, 2048, layout.rope_rows(128, 64)))
     x = {k: (torch.randn(128, k, generator=g, device=DEV)).to(torch.bfloat16).view(torch.int16) for k in (2048, 8192)}
@@ -48,6 +48,7 @@ def run_all(W, x, h, m):
     harness.gemm_residual(W["down"], layout.lane_tiles(x[8192][:m]), hd, m)
     out["down"] = digest(hd)
     out["gate_up"] = digest(harness.mlp13(W["w1"], W["w3"], xt, m))
+    out["gate_up1"] = digest(harness.mlp13(W["w1b"], W["w3b"], xt, m))  # Llama-3.2-1B shape: a single split
     out["lm"] = digest(harness.lm_greedy(W["lm"], xt, m, 3990))
     out["lm1"] = digest(harness.lm_greedy(W["lm1"], xt, m, 16390))  # a single split
     out["lm1_full"] = digest(harness.lm_full(W["lm1"], xt, m))

@@ -128,7 +128,10 @@ def test_lm_full(exact, m, n, k):
     assert np.all(err <= tol_matrix(x, w)), f"max err {err.max()}"
 
 
-@pytest.mark.parametrize("m,n,k", [(1, 256, 2048), (9, 128, 2048), (128, 64, 2048), (150, 64, 512), (9, 128, 2064)])
+# n = 8192 is the Llama-3.2-1B gate/up shape (a single split); M = 5 / 140 / 290 run the
+# streaming, register-streamed and ten-lane-tile configurations.
+@pytest.mark.parametrize("m,n,k", [(1, 256, 2048), (9, 128, 2048), (128, 64, 2048), (150, 64, 512), (9, 128, 2064),
+                                   (5, 8192, 2048), (140, 8192, 2048), (290, 8192, 2048)])
 def test_mlp13(exact, m, n, k):
     w1 = synth.bf16_normal(3, Ids.W1, n, k, 0.02)
     w3 = synth.bf16_normal(3, Ids.W3, n, k, 0.02)
@@ -168,24 +171,28 @@ def test_lm_greedy_planted(exact):
     assert np.array_equal(bi.numpy(), ri)
 
 
-def test_lm_greedy_agreement(exact):
+# n = 4096 gets eight splits; n = 16400 is a single-split head like the real one,
+# served at M = 160 and 290 by the register-streamed kernel.
+@pytest.mark.parametrize("n,vocab,m", [(4096, 4000, 300), (16400, 16390, 160), (16400, 16390, 290)])
+def test_lm_greedy_agreement(exact, n, vocab, m):
     """Random logits: argmax must agree on >= 99.9% of rows; a disagreement is
     only allowed where the oracle's top two logits are within the tolerance."""
-    n, k, vocab, m = 4096, 2048, 4000, 300
+    k = 2048
     w = synth.bf16_normal(5, Ids.LM, n, k, 0.02)
     xb = synth.bf16_normal(5, Ids.X, m, k, 1.0)
     x = synth.bf16_to_f32(xb)
-    say("lm_greedy agreement")
+    say("lm_greedy agreement", n, vocab, m)
     best = harness.lm_greedy(dev_u16(layout.pack_tiles(w)), dev_u16(layout.lane_tiles(xb)), m, vocab)
     torch.cuda.synchronize()
     _, bi = harness.best_split(best)
     _, ri = exact.lm_greedy(w, vocab, x)
     agree = np.mean(bi.numpy() == ri)
-    assert agree >= 0.999, agree
     logits = exact.gemm(w[:vocab], x)
     tol = tol_matrix(x, w[:vocab])
     for j in np.nonzero(bi.numpy() != ri)[0]:
         assert logits[j, ri[j]] - logits[j, bi[j]] <= tol[j, ri[j]] + tol[j, bi[j]]
+    # >= 99.9 % of rows; below 1000 rows a (tolerance-justified) miss is one row
+    assert agree >= 0.999 or np.sum(bi.numpy() != ri) <= 1, agree
 
 
 @pytest.mark.parametrize("D,nq,nkv,k,m,page", [(64, 512, 128, 2048, 5, 64), (64, 256, 128, 2048, 40, 16),
