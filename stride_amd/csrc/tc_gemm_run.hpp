@@ -425,9 +425,15 @@ void launch_pipe(Geometry g, const typename Epi::Out& o, int smax, hipStream_t s
   X(30, 4, 4, 2, 4, 1, 6, 1, 0) \
   X(31, 4, 8, 2, 2, 1, 4, 1, 0) \
   X(32, 3, 4, 4, 2, 2, 3, 1, 2) \
-  X(33, 6, 2, 2, 4, 2, 3, 1, 2)
+  X(33, 6, 2, 2, 4, 2, 3, 1, 2) \
+  X(34, 4, 2, 2, 4, 2, 3, 1, 0) \
+  X(35, 2, 4, 4, 2, 2, 3, 1, 0) \
+  X(36, 4, 2, 2, 4, 1, 6, 1, 0) \
+  X(37, 2, 4, 4, 2, 1, 6, 1, 0) \
+  X(38, 4, 2, 2, 4, 1, 4, 2, 0) \
+  X(39, 2, 2, 4, 4, 2, 3, 1, 0)
 
-constexpr int kNumPipeCfgs = 34;
+constexpr int kNumPipeCfgs = 40;
 extern int g_forced_pipe;
 
 template <class Epi>
@@ -556,7 +562,11 @@ inline Pick pick_large(const Geometry& g, int T, int smax, int mats, int per) {
   if (g.nseg == 3) {  // fused QKV
     if (T <= 12) return {0, 33};
     if (T <= 24) return {0, 29};
-    if (T <= 64) return {1, 14};
+    if (T <= 40) return {1, 14};
+    // 16 waves on 128 x 128 blocks: 25.6 / 26.1 / 28.2 us at M = 768 / 1024 / 1280
+    // (against 33-37); again at M = 2560 (52.4 against 68.1), where it quantizes onto
+    // the CUs better than the straddling blocks below.
+    if (T <= 80 || (T > 144 && T <= 176)) return {1, 39};
     // 12-row-tile blocks straddling the q/k/v segments: the 192 row tiles make
     // 16 row blocks, 256 workgroups at M = 2048 (the segment-aligned blocks give
     // 192 or 384): 39.0 against 46.5 us at M = 2048, 76.9 against 89.5 at 4096.
@@ -567,13 +577,15 @@ inline Pick pick_large(const Geometry& g, int T, int smax, int mats, int per) {
     if (T <= 12) return {0, 27};
     if (T <= 32) return {0, 29};
     if (T <= 64) return {0, 30};
-    return {1, pick_pipe(g, smax)};
+    if (T <= 128) return {1, 39};  // 16 waves on 128 x 128: 77.6-78.4 against 86-87 us at M = 1280-2048
+    if (T <= 160) return {1, 33};  // 12-row-tile blocks: 101 against 164 us at M = 2560
+    return {1, 8};                 // 256 x 128 blocks: 123-125 us at M = 3072-4096 (164-167 before)
   }
   if (T <= 12) return {0, 27};
   if (T <= 32) return {0, 29};
-  if (T <= 64) return {1, 12};
-  if (T <= 96) return {1, 14};
-  if (T <= 128) return {1, 0};
+  if (T <= 64) return {1, 14};
+  if (T <= 128) return {1, 39};  // 16 waves on 128 x 128: 26.0-28.3 against 32.7-35.6 us at M = 1280-2048 (O)
+  if (T <= 160) return {1, 33};  // 12-row-tile blocks: 37.4 against 42.3 us at M = 2560
   return {1, 2};
 }
 
