@@ -293,6 +293,11 @@ int stride_tc_split_count(int32_t n, int32_t k);
  * identical bits; this only changes speed. A configuration that cannot serve a
  * launch is ignored for it. */
 int stride_tc_set_stream_config(int32_t index);
+/* Tuning hook for experiments with the split rule: the K split count of matrices
+ * with N <= 4096 (default 4; 1, 2, 4, 8 or 16). Process-wide. Unlike the
+ * configuration hook this CHANGES the reduction tree and hence the bits: results
+ * are batch-invariant only between launches made under the same setting. */
+int stride_tc_set_split_rule(int32_t splits);
 int stride_tc_stream_config_count(void);
 /* Number of LDS-pipelined configurations (selected as -3-i above). */
 int stride_tc_pipe_config_count(void);

@@ -20,7 +20,7 @@
 //             and combine the split partials through LDS in ascending order. With
 //             XS, each workgroup runs one split and the last one to finish a tile
 //             group folds the partials in order. Serves decode batches and, for
-//             matrices with eight splits, prefill up to about a thousand rows.
+//             matrices with four splits, prefill up to about a thousand rows.
 //   k_pipe    LDS pipeline. WM x WN waves own a block of tiles; every stage's
 //             chunks are copied HBM->LDS by global_load_lds in fragment order
 //             through an NS-deep ring; splits are walked in order and folded in
@@ -97,6 +97,7 @@ ScratchSet scratch_for(hipStream_t st) {
 }
 
 int g_forced_cfg = -1;
+int g_split_few = 4;
 int g_forced_dec = -1;
 int g_forced_pipe = -1;
 int g_last_cfg = -1;
@@ -211,6 +212,13 @@ int stride_tc_set_stream_config(int32_t index) {
   if (index < -1 || index >= kNumDecodeCfgs) return fail(STRIDE_TC_EINVAL, "config index out of range");
   g_forced_cfg = index;
   g_forced_pipe = g_forced_dec = -1;
+  return 0;
+}
+
+int stride_tc_set_split_rule(int32_t splits) {
+  if (splits != 1 && splits != 2 && splits != 4 && splits != 8 && splits != 16)
+    return fail(STRIDE_TC_EINVAL, "split rule: splits must be 1, 2, 4, 8 or 16");
+  g_split_few = splits;
   return 0;
 }
 

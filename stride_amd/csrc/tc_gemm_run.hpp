@@ -30,15 +30,19 @@ int fail(int code, const std::string& msg);
 
 
 // The fixed K-split for an N x K weight matrix. Matrices with few row tiles
-// (N <= 4096: Q, K, V, output, down) get 8 splits so that a decode launch has
-// enough independent weight streams; larger ones (gate and up at N = 8192, the
+// (N <= 4096: Q, K, V, output, down) get 4 splits so that a decode launch has
+// enough independent weight streams (measured on MI355X against 2 and 8: at
+// M = 128, 8 splits cost 8 % more time on QKV, O and down, 2 splits 5-35 % more;
+// prefill is equal or faster with 4); larger ones (gate and up at N = 8192, the
 // LM head) get 1: they have row tiles enough for the decode launches, and a
 // single split lets the prefill kernels keep one accumulator per tile instead
 // of a split partial and a running sum. S is then capped by the chunk count and
 // halved until it divides it.
+extern int g_split_few;  // splits of matrices with N <= 4096 (tuning hook; default 8)
+
 inline int split_count(int n, int k) {
   const int chunks = k / kChunkCols;
-  int s = n <= 4096 ? 8 : 1;
+  int s = n <= 4096 ? g_split_few : 1;
   if (s > chunks) s = chunks;
   while (s > 1 && chunks % s != 0) s >>= 1;
   return s < 1 ? 1 : s;
@@ -524,6 +528,16 @@ inline Pick pick_small(int T, int smax, int mats, int nseg, int per) {
     if (T <= 4) return {1, 14};
     return {3, 10};
   }
+  if (smax == 4) {  // the split rule's few-row matrices; per = chunks per split (down: 64, O and QKV: 16)
+    if (nseg == 3) return {0, T <= 1 ? 0 : (T <= 2 ? 5 : (T <= 4 ? 33 : 27))};  // QKV: 6.3 / 7.0 / 8.3 / 10.0 us at M = 1 / 32 / 64 / 128
+    if (per >= 32) {  // down: 11.2 / 11.9 / 14.5 / 16.7 us at M = 1 / 32 / 64 / 128
+      if (T <= 1) return {0, 55};
+      if (T <= 2) return {0, 0};
+      if (T <= 4) return {0, 5};
+      return {3, 7};
+    }
+    return {0, T <= 2 ? 0 : (T <= 4 ? 5 : 33)};  // O: 5.1 / 5.0 / 5.7 / 7.1 us at M = 1 / 32 / 64 / 128
+  }
   if (smax == 1 && T <= 2) return {3, 10};
   if (smax == 1 && T >= 3 && T <= 4) return {3, 8};
   if (smax == 1 && T == 8) return {3, 12};
@@ -534,7 +548,7 @@ inline Pick pick_small(int T, int smax, int mats, int nseg, int per) {
   return {0, pick_decode(T, smax, mats, nseg, per)};
 }
 
-// More than 8 lane tiles. Matrices with eight splits (QKV, O, down) have few row
+// More than 8 lane tiles. Matrices with several splits (QKV, O, down) have few row
 // tiles and long split chains: up to a few hundred rows the streaming kernel,
 // whose waves run the splits side by side, beats the pipeline, which walks them
 // one after another; beyond, the pipeline with a block shape per size.
@@ -558,6 +572,34 @@ inline Pick pick_large(const Geometry& g, int T, int smax, int mats, int per) {
     if (T <= 48) return {1, 2};
     if (T <= 64) return {1, pick_pipe(g, smax)};
     return {1, 28};
+  }
+  if (smax == 4) {  // the split rule's few-row matrices (sweeps at M = 160 ... 4096)
+    if (g.nseg == 3) {  // fused QKV
+      if (T <= 10) return {0, 33};   // 12.6 us at M = 160
+      if (T <= 12) return {0, 15};   // 13.6 us at M = 192
+      if (T <= 19) return {0, 29};   // 14.1-14.2 us at M = 256-290
+      if (T <= 24) return {1, 15};   // 17.8 us at M = 384
+      if (T <= 32) return {1, 12};   // 19.1 us at M = 512
+      if (T <= 80) return {1, 39};   // 16 waves on 128 x 128: 25.2 / 25.9 / 28.3 us at M = 768 / 1024 / 1280
+      if (T <= 128) return {1, 33};  // straddling 12-row-tile blocks: 35.9 / 40.3 us at M = 1536 / 2048
+      return {1, 38};                // 46.4 / 67.2 / 74.2 us at M = 2560 / 3072 / 4096
+    }
+    if (per >= 32) {  // down
+      if (T <= 16) return {3, 1};    // 20.3 / 20.7 / 23.3 us at M = 160 / 192 / 256
+      if (T <= 32) return {3, 2};    // 26.4 / 29.4 / 30.8 us at M = 290 / 384 / 512
+      if (T <= 64) return {0, 30};   // 49.4 / 49.9 us at M = 768 / 1024
+      if (T <= 128) return {1, 39};  // 75.6 / 75.8 / 78.8 us at M = 1280 / 1536 / 2048
+      if (T <= 160) return {1, 33};  // 100.2 us at M = 2560
+      return {1, 23};                // 117.3 / 121.5 us at M = 3072 / 4096
+    }
+    // O
+    if (T <= 16) return {0, 27};     // 8.7 / 9.0 / 9.1 us at M = 160 / 192 / 256
+    if (T <= 32) return {0, 29};     // 12.7 / 12.8 / 12.8 us at M = 290 / 384 / 512
+    if (T <= 48) return {1, 14};     // 17.7 us at M = 768
+    if (T <= 64) return {0, 30};     // 18.6 us at M = 1024
+    if (T <= 128) return {1, 39};    // 23.9 / 24.1 / 27.1 us at M = 1280 / 1536 / 2048
+    if (T <= 160) return {1, 33};    // 34.6 us at M = 2560
+    return {1, 28};                  // 39.2 / 44.1 us at M = 3072 / 4096
   }
   if (g.nseg == 3) {  // fused QKV
     if (T <= 12) return {0, 33};

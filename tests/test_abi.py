@@ -104,10 +104,10 @@ def test_exact_struct_layout_matches_reference(tmp_path):
 
 
 def test_split_rule():
-    cases = {(2048, 2048): 8, (3072, 2048): 8, (512, 2048): 8, (2048, 8192): 8, (8192, 2048): 1, (4096, 2048): 8, (4112, 2048): 1,
-             (128256, 2048): 1, (16, 64): 2, (16, 32): 1, (64, 96): 3, (64, 160): 5, (64, 192): 6,
+    cases = {(2048, 2048): 4, (3072, 2048): 4, (512, 2048): 4, (2048, 8192): 4, (8192, 2048): 1, (4096, 2048): 4, (4112, 2048): 1,
+             (128256, 2048): 1, (16, 64): 2, (16, 32): 1, (64, 96): 3, (64, 160): 1, (64, 192): 2, (64, 256): 4,
              # K = 16 (mod 32): whole chunks decide, the half chunk joins the last split
-             (16, 48): 1, (16, 16): 1, (2048, 2064): 8, (8192, 2064): 1, (64, 112): 3}
+             (16, 48): 1, (16, 16): 1, (2048, 2064): 4, (8192, 2064): 1, (64, 112): 3}
     for (n, k), s in cases.items():
         assert tc.split_count(n, k) == s, (n, k)
     with pytest.raises(_lib.StrideTcError):

@@ -171,7 +171,7 @@ def test_lm_greedy_planted(exact):
     assert np.array_equal(bi.numpy(), ri)
 
 
-# n = 4096 gets eight splits; n = 16400 is a single-split head like the real one,
+# n = 4096 gets four splits; n = 16400 is a single-split head like the real one,
 # served at M = 160 and 290 by the register-streamed kernel.
 @pytest.mark.parametrize("n,vocab,m", [(4096, 4000, 300), (16400, 16390, 160), (16400, 16390, 290)])
 def test_lm_greedy_agreement(exact, n, vocab, m):
@@ -235,7 +235,7 @@ def test_qkv(exact, D, nq, nkv, k, m, page):
 def test_half_chunk_rows_are_batch_invariant():
     """K = 2064 (16 mod 32): every output row has the same bits at M = 1, 37,
     128 and 300 (the largest as the reference) and under a row permutation, for
-    the residual GEMM (8 splits) and the LM head (1 split, greedy and full)."""
+    the residual GEMM (4 splits) and the LM head (1 split, greedy and full)."""
     import hashlib
 
     n, k = 2048, 2064
