@@ -226,7 +226,7 @@ __global__ __launch_bounds__(64) void k_attn_page(StrideAttentionParams p, int p
 #pragma unroll
   for (int k = 0; k < kPer; ++k) {
     const int P = k * 64 + lane, i = P / (D / kEl), c = P % (D / kEl);
-    vr[k] = load16(kv_row<KvT>(p.kv, page_shift, p.layer, 1, g, slot, min(p0 + i, last)) + c * kEl);
+    vr[k] = ld_kv(kv_row<KvT>(p.kv, page_shift, p.layer, 1, g, slot, min(p0 + i, last)) + c * kEl);
   }
   {
     const KvT* key = kv_row<KvT>(p.kv, page_shift, p.layer, 0, g, slot, min(p0 + lane, last));
@@ -401,7 +401,7 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_fused(StrideAttentionParams p
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
       const int P = k * 64 + lane, i = P / (D / kEl), c = P % (D / kEl);
-      vr[k] = load16(kv_at(1, min(p0 + i, last)) + c * kEl);
+      vr[k] = ld_kv(kv_at(1, min(p0 + i, last)) + c * kEl);
     }
     const uint16_t* key = kv_at(0, min(p0 + lane, last));
 #pragma unroll

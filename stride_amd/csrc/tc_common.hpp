@@ -64,6 +64,26 @@ __device__ __forceinline__ int frag_lane_of_piece(int j) {
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
 __device__ __forceinline__ u32x4 load16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+// Streamed operands are read once per launch: weight chunks (each wave
+// instruction reads one whole 1 KiB chunk) and V rows of attention pages.
+// STRIDE_TC_WNT / STRIDE_TC_KVNT = 1 issues their loads with the non-temporal
+// hint. (K rows are not: a lane reads its 128-byte K row 16 bytes at a time over
+// eight instructions, which the hint would turn into eight fetches of the line.)
+#ifndef STRIDE_TC_WNT
+#define STRIDE_TC_WNT 1
+#endif
+#ifndef STRIDE_TC_KVNT
+#define STRIDE_TC_KVNT 1
+#endif
+template <int NT = STRIDE_TC_WNT>
+__device__ __forceinline__ u32x4 ld_weight(const void* p) {
+  if constexpr (NT != 0) return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  else return load16(p);
+}
+__device__ __forceinline__ u32x4 ld_kv(const void* p) {
+  if constexpr (STRIDE_TC_KVNT) return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  else return load16(p);
+}
 
 __device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);

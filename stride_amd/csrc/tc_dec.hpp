@@ -37,7 +37,7 @@
 
 namespace stride_tc {
 
-template <class Epi, int R, int LT, int NW, int KC, int NSS, bool XS, int WS, int OCC>
+template <class Epi, int R, int LT, int NW, int KC, int NSS, bool XS, int WS, int OCC, int WNT>
 __global__ __launch_bounds__(kWave * NW, OCC) void k_dec(Geometry g, typename Epi::Out o) {
   static_assert(!(XS && Epi::kReduce), "the argmax epilogue needs whole tiles");
   static_assert(NSS >= 2, "at least one stage in flight");
@@ -145,7 +145,7 @@ __global__ __launch_bounds__(kWave * NW, OCC) void k_dec(Geometry g, typename Ep
       for (int m = 0; m < M; ++m)
 #pragma unroll
         for (int r = 0; r < R; ++r)
-          wb[s][kc][m][r] = load16(wp[m][r] + static_cast<int64_t>(stage * KC + kc) * kChunkBytes);
+          wb[s][kc][m][r] = ld_weight<WNT>(wp[m][r] + static_cast<int64_t>(stage * KC + kc) * kChunkBytes);
   };
 
   f32x4 acc[M][R][LT];

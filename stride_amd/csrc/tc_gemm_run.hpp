@@ -230,39 +230,50 @@ inline bool decode_cfg_fits(const DecodeCfg& c, Geometry g, int smax, int mats, 
 // Configurations of k_dec (weights to registers, activations through an LDS
 // ring): (R row tiles per wave, LT lane tiles, NW waves, KC chunks per stage,
 // NSS ring slots, XS one split per workgroup, WS split groups per workgroup, OCC
-// workgroups per CU the register allocation is bounded for). Index 1000 + i in the tuning hook
+// workgroups per CU the register allocation is bounded for, WNT weight loads with
+// the non-temporal hint). Configurations 23-30 repeat 1, 2, 12, 14, 16, 19, 22
+// and 7 with plain weight loads, for launches whose lane groups re-read each
+// weight chunk from L2 (where the hint costs HBM re-reads). Index 1000 + i in the tuning hook
 // selects configuration i.
 #define STRIDE_TC_DEC_CONFIGS(D)       \
-  D(0, 1, 8, 4, 2, 4, true, 1, 1)     \
-  D(1, 1, 8, 4, 1, 8, true, 1, 1)     \
-  D(2, 1, 8, 8, 2, 4, true, 1, 1)     \
-  D(3, 1, 8, 4, 2, 4, false, 2, 1)    \
-  D(4, 1, 8, 4, 2, 4, false, 1, 1)    \
-  D(5, 2, 8, 4, 2, 4, false, 1, 1)    \
-  D(6, 1, 4, 4, 2, 4, true, 1, 1)     \
-  D(7, 1, 4, 4, 1, 8, true, 1, 1)     \
-  D(8, 2, 4, 4, 2, 4, false, 1, 1)    \
-  D(9, 1, 8, 4, 1, 8, false, 2, 1)    \
-  D(10, 1, 4, 4, 2, 4, false, 1, 1)   \
-  D(11, 1, 4, 4, 2, 4, false, 2, 1)   \
-  D(12, 2, 8, 4, 1, 4, false, 1, 2)   \
-  D(13, 1, 4, 4, 1, 8, false, 2, 1)   \
-  D(14, 2, 8, 4, 1, 8, false, 1, 1)   \
-  D(15, 1, 2, 2, 2, 4, true, 1, 1)    \
-  D(16, 1, 8, 4, 1, 4, false, 1, 2)   \
-  D(17, 2, 8, 4, 1, 6, false, 1, 2)   \
-  D(18, 2, 4, 4, 2, 4, false, 1, 2)   \
-  D(19, 4, 4, 4, 1, 4, false, 1, 2)   \
-  D(20, 1, 8, 4, 1, 4, false, 2, 2)   \
-  D(21, 2, 8, 8, 1, 4, false, 1, 1)   \
-  D(22, 1, 10, 4, 2, 4, false, 1, 1)
+  D(0, 1, 8, 4, 2, 4, true, 1, 1, 1)     \
+  D(1, 1, 8, 4, 1, 8, true, 1, 1, 1)     \
+  D(2, 1, 8, 8, 2, 4, true, 1, 1, 1)     \
+  D(3, 1, 8, 4, 2, 4, false, 2, 1, 1)    \
+  D(4, 1, 8, 4, 2, 4, false, 1, 1, 1)    \
+  D(5, 2, 8, 4, 2, 4, false, 1, 1, 1)    \
+  D(6, 1, 4, 4, 2, 4, true, 1, 1, 1)     \
+  D(7, 1, 4, 4, 1, 8, true, 1, 1, 1)     \
+  D(8, 2, 4, 4, 2, 4, false, 1, 1, 1)    \
+  D(9, 1, 8, 4, 1, 8, false, 2, 1, 1)    \
+  D(10, 1, 4, 4, 2, 4, false, 1, 1, 1)   \
+  D(11, 1, 4, 4, 2, 4, false, 2, 1, 1)   \
+  D(12, 2, 8, 4, 1, 4, false, 1, 2, 1)   \
+  D(13, 1, 4, 4, 1, 8, false, 2, 1, 1)   \
+  D(14, 2, 8, 4, 1, 8, false, 1, 1, 1)   \
+  D(15, 1, 2, 2, 2, 4, true, 1, 1, 1)    \
+  D(16, 1, 8, 4, 1, 4, false, 1, 2, 1)   \
+  D(17, 2, 8, 4, 1, 6, false, 1, 2, 1)   \
+  D(18, 2, 4, 4, 2, 4, false, 1, 2, 1)   \
+  D(19, 4, 4, 4, 1, 4, false, 1, 2, 1)   \
+  D(20, 1, 8, 4, 1, 4, false, 2, 2, 1)   \
+  D(21, 2, 8, 8, 1, 4, false, 1, 1, 1)   \
+  D(22, 1, 10, 4, 2, 4, false, 1, 1, 1) \
+  D(23, 1, 8, 4, 1, 8, true, 1, 1, 0)   \
+  D(24, 1, 8, 8, 2, 4, true, 1, 1, 0)   \
+  D(25, 2, 8, 4, 1, 4, false, 1, 2, 0)  \
+  D(26, 2, 8, 4, 1, 8, false, 1, 1, 0)  \
+  D(27, 1, 8, 4, 1, 4, false, 1, 2, 0)  \
+  D(28, 4, 4, 4, 1, 4, false, 1, 2, 0)  \
+  D(29, 1, 10, 4, 2, 4, false, 1, 1, 0) \
+  D(30, 1, 4, 4, 1, 8, true, 1, 1, 0)
 
 struct DecCfg {
   int r, lt, nw, kc, nss;
   bool xs;
-  int ws, occ;
+  int ws, occ, wnt;
 };
-#define STRIDE_TC_DEC_ROW(i, R, LT, NW, KC, NSS, XS, WS, OCC) {R, LT, NW, KC, NSS, XS, WS, OCC},
+#define STRIDE_TC_DEC_ROW(i, R, LT, NW, KC, NSS, XS, WS, OCC, WNT) {R, LT, NW, KC, NSS, XS, WS, OCC, WNT},
 constexpr DecCfg kDecCfgs[] = {STRIDE_TC_DEC_CONFIGS(STRIDE_TC_DEC_ROW)};
 #undef STRIDE_TC_DEC_ROW
 constexpr int kNumDecCfgs = sizeof(kDecCfgs) / sizeof(kDecCfgs[0]);
@@ -290,7 +301,7 @@ inline bool dec_cfg_fits(const DecCfg& c, const Geometry& g, int smax, int mats,
   return true;
 }
 
-template <class Epi, int R, int LT, int NW, int KC, int NSS, bool XS, int WS, int OCC>
+template <class Epi, int R, int LT, int NW, int KC, int NSS, bool XS, int WS, int OCC, int WNT>
 void launch_dec(Geometry g, const typename Epi::Out& o, hipStream_t st) {
   if constexpr ((XS || WS > 1) && Epi::kReduce) {
     return;  // never selected (dec_cfg_fits)
@@ -302,16 +313,16 @@ void launch_dec(Geometry g, const typename Epi::Out& o, hipStream_t st) {
       blocks += XS ? g.seg[i].blocks * g.seg[i].splits : g.seg[i].blocks;
     }
     blocks *= (g.lane_groups + LT - 1) / LT;
-    hipLaunchKernelGGL((k_dec<Epi, R, LT, NW, KC, NSS, XS, WS, OCC>), dim3(blocks), dim3(kWave * NW), 0, st, g, o);
+    hipLaunchKernelGGL((k_dec<Epi, R, LT, NW, KC, NSS, XS, WS, OCC, WNT>), dim3(blocks), dim3(kWave * NW), 0, st, g, o);
   }
 }
 
 template <class Epi>
 void launch_dec_cfg(int idx, const Geometry& g, const typename Epi::Out& o, hipStream_t st) {
   switch (idx) {
-#define STRIDE_TC_DEC_CASE(i, R, LT, NW, KC, NSS, XS, WS, OCC) \
-  case i:                                                       \
-    launch_dec<Epi, R, LT, NW, KC, NSS, XS, WS, OCC>(g, o, st); \
+#define STRIDE_TC_DEC_CASE(i, R, LT, NW, KC, NSS, XS, WS, OCC, WNT) \
+  case i:                                                            \
+    launch_dec<Epi, R, LT, NW, KC, NSS, XS, WS, OCC, WNT>(g, o, st); \
     break;
     STRIDE_TC_DEC_CONFIGS(STRIDE_TC_DEC_CASE)
 #undef STRIDE_TC_DEC_CASE
@@ -534,14 +545,15 @@ inline Pick pick_small(int T, int smax, int mats, int nseg, int per) {
       if (T <= 1) return {0, 55};
       if (T <= 2) return {0, 0};
       if (T <= 4) return {0, 5};
-      return {3, 7};
+      return {3, 30};  // plain weight loads (two lane groups share them through L2): 16.7 us at M = 128
     }
     return {0, T <= 2 ? 0 : (T <= 4 ? 5 : 33)};  // O: 5.1 / 5.0 / 5.7 / 7.1 us at M = 1 / 32 / 64 / 128
   }
   if (smax == 1 && T <= 2) return {3, 10};
   if (smax == 1 && T >= 3 && T <= 4) return {3, 8};
   if (smax == 1 && T == 8) return {3, 12};
-  if (smax == 1 && T >= 2) return {1, T <= 4 ? 14 : 8};
+  if (smax == 1 && T >= 5) return {3, 12};  // LM head at M = 65-128: 101.6 us at M = 96 (pipeline: 117.9)
+  if (smax == 1 && T >= 2) return {1, 14};
   if (smax == 2 && mats == 2 && T >= 2 && T <= 4) return {3, 13};
   if (smax == 2 && mats == 2 && T >= 3) return {1, 15};
   if (smax == 8 && nseg == 1 && per >= 32 && T >= 2 && T <= 4) return {3, 7};  // long splits (down), one split per workgroup
@@ -554,16 +566,17 @@ inline Pick pick_small(int T, int smax, int mats, int nseg, int per) {
 // one after another; beyond, the pipeline with a block shape per size.
 inline Pick pick_large(const Geometry& g, int T, int smax, int mats, int per) {
   if (smax == 1 && mats == 2) {  // gate/up (single split)
-    if (T <= 16) return {3, 4};   // 25.1-25.5 us at M = 160-256
-    if (T <= 20) return {3, 22};  // ten lane tiles per workgroup: 30.7 us at M = 290 (pipeline: 35.5)
-    if (T <= 24) return {1, 26};
-    if (T <= 40) return {1, 23};  // 40.2 us at M = 512
+    if (T <= 16) return {3, 16};  // 24.6 / 24.1 / 26.1 us at M = 160 / 192 / 256
+    if (T <= 20) return {3, 22};  // ten lane tiles per workgroup: 30.1 us at M = 290 (pipeline: 35.5)
+    if (T <= 32) return {3, 14};  // 37.9 / 40.5 us at M = 384 / 512
+    if (T <= 40) return {1, 23};
     return {1, 4};                // 256 x 256 blocks: 63.0 / 122.5 / 233.4 us at M = 1024 / 2048 / 4096
   }
   if (smax == 1) {  // LM head: weights to registers at 9-12 and 17-24 lane tiles (M = 160 / 290 / 384:
                     // 150 / 205 / 226 us against 186 / 269 / 263 with the pipeline), 256 x 256 blocks otherwise
-    if (T <= 12 || (T > 16 && T <= 20)) return {3, 19};
-    if (T > 20 && T <= 24) return {3, 14};
+    // several lane groups re-read each weight chunk: plain weight loads
+    if (T <= 12 || (T > 16 && T <= 20)) return {3, 28};  // 148 / 152 / 216 us at M = 160 / 192 / 290
+    if (T > 20 && T <= 24) return {3, 25};               // 239 us at M = 384
     return {1, 6};
   }
   if (smax == 2) {
@@ -585,8 +598,9 @@ inline Pick pick_large(const Geometry& g, int T, int smax, int mats, int per) {
       return {1, 38};                // 46.4 / 67.2 / 74.2 us at M = 2560 / 3072 / 4096
     }
     if (per >= 32) {  // down
-      if (T <= 16) return {3, 1};    // 20.3 / 20.7 / 23.3 us at M = 160 / 192 / 256
-      if (T <= 32) return {3, 2};    // 26.4 / 29.4 / 30.8 us at M = 290 / 384 / 512
+      if (T <= 16) return {3, 23};   // 22.1 / 22.1 / 23.6 us at M = 160 / 192 / 256
+      if (T <= 20) return {3, 24};   // 26.8 us at M = 290
+      if (T <= 32) return {3, 2};    // 29.1 / 30.6 us at M = 384 / 512
       if (T <= 64) return {0, 30};   // 49.4 / 49.9 us at M = 768 / 1024
       if (T <= 128) return {1, 39};  // 75.6 / 75.8 / 78.8 us at M = 1280 / 1536 / 2048
       if (T <= 160) return {1, 33};  // 100.2 us at M = 2560

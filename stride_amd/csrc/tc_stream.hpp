@@ -273,7 +273,7 @@ __global__ __launch_bounds__(kWave * WS * WR) void k_stream(Geometry g, typename
 #pragma unroll
       for (int m = 0; m < M; ++m)
 #pragma unroll
-        for (int r = 0; r < R; ++r) a[u][m][r] = load16(wp[m][r] + static_cast<int64_t>(c + u) * kChunkBytes);
+        for (int r = 0; r < R; ++r) a[u][m][r] = ld_weight(wp[m][r] + static_cast<int64_t>(c + u) * kChunkBytes);
   };
   auto load_x = [&](u32x4 (&bx)[XL ? 1 : U][LT], int c) {
     if constexpr (!XL) {
@@ -364,7 +364,7 @@ __global__ __launch_bounds__(kWave * WS * WR) void k_stream(Geometry g, typename
 #pragma unroll
         for (int m = 0; m < M; ++m)
 #pragma unroll
-          for (int r = 0; r < R; ++r) acc[m][r][l] = mfma(load16(wp[m][r] + static_cast<int64_t>(c) * kChunkBytes), bv, acc[m][r][l]);
+          for (int r = 0; r < R; ++r) acc[m][r][l] = mfma(ld_weight(wp[m][r] + static_cast<int64_t>(c) * kChunkBytes), bv, acc[m][r][l]);
       }
     }
   }
@@ -383,7 +383,7 @@ __global__ __launch_bounds__(kWave * WS * WR) void k_stream(Geometry g, typename
       for (int m = 0; m < M; ++m)
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-          const u32x4 av = lane < 32 ? load16(wp[m][r] + tail) : zero;
+          const u32x4 av = lane < 32 ? ld_weight(wp[m][r] + tail) : zero;
           acc[m][r][l] = mfma(av, bv, acc[m][r][l]);
         }
     }

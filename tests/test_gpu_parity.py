@@ -96,7 +96,9 @@ def test_config1_bf16_rounding_alone_fails_the_bound(exact):
 @pytest.mark.parametrize("m,n,k", [(1, 256, 2048), (5, 128, 2048), (16, 64, 8192), (17, 256, 2048), (64, 128, 2048),
                                    (130, 128, 1024), (290, 256, 2048), (33, 48, 96),
                                    # K = 16 (mod 32): a trailing half chunk
-                                   (37, 128, 48), (1, 2048, 2064), (130, 256, 2064), (300, 64, 16)])
+                                   (37, 128, 48), (1, 2048, 2064), (130, 256, 2064), (300, 64, 16),
+                                   # the Llama-3.2-1B O and down shapes at the benchmark's M = 128
+                                   (128, 2048, 2048), (128, 2048, 8192)])
 def test_gemm_residual(exact, m, n, k):
     w, xb, x = make(1, m, n, k)
     h = synth.f32_normal(1, Ids.H, m, n)
@@ -196,7 +198,8 @@ def test_lm_greedy_agreement(exact, n, vocab, m):
 
 
 @pytest.mark.parametrize("D,nq,nkv,k,m,page", [(64, 512, 128, 2048, 5, 64), (64, 256, 128, 2048, 40, 16),
-                                              (16, 64, 32, 256, 21, 16), (64, 256, 128, 2064, 21, 16)])
+                                              (16, 64, 32, 256, 21, 16), (64, 256, 128, 2064, 21, 16),
+                                              (64, 2048, 512, 2048, 128, 16)])  # the Llama-3.2-1B QKV shape, M = 128
 def test_qkv(exact, D, nq, nkv, k, m, page):
     wq = synth.bf16_normal(6, Ids.WQ, nq, k, 0.02)
     wk = synth.bf16_normal(6, Ids.WK, nkv, k, 0.02)
