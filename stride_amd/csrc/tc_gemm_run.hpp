@@ -131,7 +131,8 @@ inline bool mat_ok(const StrideGemmMat& m, const char* name, std::string& why) {
   S(55, 1, 1, 1, 2, 8, false, true) \
   S(56, 2, 1, 1, 4, 4, false, true) \
   S(57, 1, 2, 1, 4, 8, false, true) \
-  S(58, 1, 8, 1, 4, 8, false, true)
+  S(58, 1, 8, 1, 4, 8, false, true) \
+  S(59, 2, 2, 4, 1, 4, false, false)
 
 struct DecodeCfg {
   int r, lt, ws, wr, u;
@@ -588,7 +589,7 @@ inline Pick pick_large(const Geometry& g, int T, int smax, int mats, int per) {
   }
   if (smax == 4) {  // the split rule's few-row matrices (sweeps at M = 160 ... 4096)
     if (g.nseg == 3) {  // fused QKV
-      if (T <= 10) return {0, 33};   // 12.6 us at M = 160
+      if (T <= 10) return {0, 59};   // four split waves for the four splits: 10.6 us at M = 160 (12.5 with eight)
       if (T <= 12) return {0, 15};   // 13.6 us at M = 192
       if (T <= 19) return {0, 29};   // 14.1-14.2 us at M = 256-290
       if (T <= 24) return {1, 15};   // 17.8 us at M = 384
@@ -608,7 +609,8 @@ inline Pick pick_large(const Geometry& g, int T, int smax, int mats, int per) {
     }
     // O
     if (T <= 16) return {0, 27};     // 8.7 / 9.0 / 9.1 us at M = 160 / 192 / 256
-    if (T <= 32) return {0, 29};     // 12.7 / 12.8 / 12.8 us at M = 290 / 384 / 512
+    if (T <= 20) return {0, 59};     // 11.9 us at M = 290
+    if (T <= 32) return {0, 29};     // 12.6 / 12.6 us at M = 384 / 512
     if (T <= 48) return {1, 14};     // 17.7 us at M = 768
     if (T <= 64) return {0, 30};     // 18.6 us at M = 1024
     if (T <= 128) return {1, 39};    // 23.9 / 24.1 / 27.1 us at M = 1280 / 1536 / 2048
