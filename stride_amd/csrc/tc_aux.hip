@@ -359,17 +359,6 @@ __global__ __launch_bounds__(256) void k_attn_combine(StrideAttentionParams p) {
 // in LDS; after a barrier the workgroup combines the records in ascending page
 // order exactly as k_attn_combine does and writes the bf16 x tiles. The page
 // records never leave the CU and no second launch is needed.
-// Ordering of LDS accesses between the lanes of one wave: the wave's earlier LDS
-// operations have completed (lgkmcnt 0) and the compiler moves no memory access
-// across. The page loop's staging buffers are per wave, so no workgroup barrier
-// is needed there; __syncthreads() would also wait for the next page's K and V
-// loads still in flight (vmcnt 0), which is what the loop prefetches them for.
-__device__ __forceinline__ void wave_lds_sync() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt left at their maxima
-  asm volatile("" ::: "memory");
-}
-
 template <int D, int NWV>
 __global__ __launch_bounds__(64 * NWV) void k_attn_fused(StrideAttentionParams p, int page_shift) {
   constexpr int kEl = 8;                        // bf16 elements per 16-byte piece
@@ -431,7 +420,7 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_fused(StrideAttentionParams p
         *reinterpret_cast<u32x4*>(&vs[wave][P / (D / kEl)][(P % (D / kEl)) * kEl]) = vr[k];
       }
     }
-    wave_lds_sync();  // this wave's V rows
+    __syncthreads();  // this wave's V rows
     f32x4 mx = {0.f, 0.f, 0.f, 0.f};
     float sc[kHeadsPerGroup] = {0.f, 0.f, 0.f, 0.f};
     if (active) {
@@ -471,7 +460,7 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_fused(StrideAttentionParams p
       if (lane < n)
         w4[wave][lane] = f32x4{det_exp(sc[0] - mx[0]), det_exp(sc[1] - mx[1]), det_exp(sc[2] - mx[2]), det_exp(sc[3] - mx[3])};
     }
-    wave_lds_sync();  // this wave's weights
+    __syncthreads();  // this wave's weights
     if (active) {
       float* rec = recs + page * RF;
       const float* wflat = reinterpret_cast<const float*>(w4[wave]);
@@ -497,9 +486,8 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_fused(StrideAttentionParams p
         rec[4 + lane] = dn;
       }
     }
-    wave_lds_sync();  // the staging buffers are reused by the next round
+    __syncthreads();  // the staging buffers are reused by the next round
   }
-  __syncthreads();  // every wave's page records
   // Combine in ascending page order (k_attn_combine's expressions). Each page
   // factor is computed by its own thread; every thread derives the head maximum
   // with the same ascending loop, so all agree; each output thread then forms
@@ -589,9 +577,6 @@ static int fused_nwv(dim3 grid, size_t lds, hipStream_t st, const StrideAttentio
 // fewer (batch 64) four waves finish a row sooner.
 template <int D>
 static int fused(dim3 grid, size_t lds, hipStream_t st, const StrideAttentionParams& p, int page_shift) {
-#ifdef STRIDE_TC_ATTN_NWV
-  return fused_nwv<D, STRIDE_TC_ATTN_NWV>(grid, lds, st, p, page_shift);
-#endif
   if (grid.x >= 768) return fused_nwv<D, 2>(grid, lds, st, p, page_shift);
   return fused_nwv<D, 4>(grid, lds, st, p, page_shift);
 }
