@@ -114,6 +114,23 @@ def test_split_rule():
         tc.split_count(16, 24)
 
 
+def test_split_rule_hook():
+    """The split-rule tuning hook (experiments only: it changes the bits) takes 1, 2,
+    4, 8 or 16 splits for the few-row matrices and nothing else; gate/up and the LM
+    head keep one split."""
+    try:
+        for s in (1, 2, 8, 16):
+            _lib.set_split_rule(s)
+            assert tc.split_count(2048, 8192) == s
+            assert tc.split_count(8192, 2048) == 1
+        for bad in (0, 3, 32, -1):
+            with pytest.raises(_lib.StrideTcError):
+                _lib.set_split_rule(bad)
+    finally:
+        _lib.set_split_rule(4)
+    assert tc.split_count(2048, 2048) == 4
+
+
 def test_rejects_bad_arguments_without_launch():
     lib = _lib.load()
     p = tc.TcGemmResidualParams(tc.Lanes(17, 1, 0, 0), 0x1000, tc.GemmMat(0x2000, 4, 64), 0x3000)
