@@ -16,7 +16,7 @@ from stride_amd import harness, layout, synth
 pytestmark = pytest.mark.gpu
 
 DEV = "cuda:0"
-MS = [1, 8, 32, 64, 128, 290, 1024, 1536, 2048, 4096]
+MS = [1, 8, 32, 64, 128, 160, 290, 1024, 1536, 2048, 4096]
 
 
 def say(*a):
