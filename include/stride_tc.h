@@ -40,7 +40,11 @@
  * recently used one), so launches on up to four streams of one device may
  * overlap; with more streams in flight at once, order them (the reference
  * keeps every launch on one stream, src/kernels.cu:457-460). A launch captured
- * in a HIP graph keeps the set of its capture stream. The configuration hooks
+ * in a HIP graph keeps the set of its capture stream for every replay, and a
+ * fifth stream used at any time later (not only at once) may be given that same
+ * set: order eager launches on such a stream with the graph's replays. Built
+ * with -DSTRIDE_TC_DEBUG, a launch that would take over a set whose stream still
+ * has work queued fails with STRIDE_TC_EINVAL instead. The configuration hooks
  * below are process-wide and meant for tuning sweeps, not for concurrent
  * callers.
  */
@@ -266,14 +270,20 @@ int stride_tc_norm(const StrideTcNormParams* p, int per_lane, void* stream);
  * written as bf16 x tiles. The KV storage page (group_elems / head_dim tokens,
  * a power of two) is independent of the 64-position summation page. head_dim
  * must be 32, 64 or 128; n_q must be 4.
- * Extension (no reference counterpart): item_count == -1 means every page of
- * every row, the list the reference's engine always builds (src/engine.cpp:
- * 93-103); then items and scratch are not read, the page records stay in LDS and
- * pages and combine run as one kernel (same bits). max_pages bounds the pages of
- * a row; max_pages * (12 + 4 * head_dim) floats, the row's KV page numbers
- * (4 bytes each) and the kernel's staging must fit 159 KiB of LDS: with 16-token
- * KV pages up to 115 pages (7360 positions) at head_dim 64, 44 at head_dim 128;
- * larger values are rejected (use an item list). */
+ * The library picks the form. With the item list the reference's engine
+ * always builds (src/engine.cpp:93-103: rows ascending, each row's pages 0 ..
+ * last ascending), up to 512 rows and when the row's records fit the LDS (below),
+ * pages and combine run as one kernel that checks each row's stretch of the list
+ * on the device; such rows keep their records in LDS and leave `scratch` as it
+ * was. Any other list gets the page + combine semantics exactly: listed pages
+ * are summed and stored in `scratch`, the rest are combined from what `scratch`
+ * holds. Extension (no reference counterpart): item_count == -1 means every page
+ * of every row with no list and no scratch. The one-kernel form needs
+ * max_pages * (12 + 4 * head_dim) floats plus the row's KV page numbers (4 bytes
+ * each) and its staging within 159 KiB of LDS: with 16-token KV pages up to 115
+ * pages (7360 positions) at head_dim 64, 44 at head_dim 128; item_count == -1
+ * beyond that is rejected, item lists beyond it run the page + combine pair.
+ * Every row must satisfy row_pos < 64 * max_pages. */
 int stride_tc_attention(const StrideAttentionParams* p, void* stream);
 
 /* Replaces stride::tc_compact (src/kernels_tc.h:85, src/kernels_tc.cu:566-587):
@@ -293,11 +303,6 @@ int stride_tc_split_count(int32_t n, int32_t k);
  * identical bits; this only changes speed. A configuration that cannot serve a
  * launch is ignored for it. */
 int stride_tc_set_stream_config(int32_t index);
-/* Tuning hook for experiments with the split rule: the K split count of matrices
- * with N <= 4096 (default 4; 1, 2, 4, 8 or 16). Process-wide. Unlike the
- * configuration hook this CHANGES the reduction tree and hence the bits: results
- * are batch-invariant only between launches made under the same setting. */
-int stride_tc_set_split_rule(int32_t splits);
 int stride_tc_stream_config_count(void);
 /* Number of LDS-pipelined configurations (selected as -3-i above). */
 int stride_tc_pipe_config_count(void);

@@ -351,15 +351,27 @@ __global__ __launch_bounds__(256) void k_attn_combine(StrideAttentionParams p) {
   }
 }
 
-// Pages and combine in one kernel, for calls that list every page of every row
-// (item_count == -1: the list the reference's engine always builds,
-// src/engine.cpp:93-103). One workgroup per (row, KV group): its NWV waves take
-// the row's 64-position pages round robin, each summing a page exactly as
-// k_attn_page does (the same expressions in the same order) into a record kept
-// in LDS; after a barrier the workgroup combines the records in ascending page
-// order exactly as k_attn_combine does and writes the bf16 x tiles. The page
-// records never leave the CU and no second launch is needed.
-template <int D, int NWV>
+// Pages and combine in one kernel. One workgroup per (row, KV group): its NWV
+// waves take the row's 64-position pages round robin, each summing a page
+// exactly as k_attn_page does (the same expressions in the same order) into a
+// record kept in LDS; after a barrier the workgroup combines the records in
+// ascending page order exactly as k_attn_combine does and writes the bf16 x
+// tiles. No second launch is needed.
+//
+// LIST = false: item_count == -1, every page of every row is computed.
+// LIST = true: the caller's (row, page) item list decides, with the semantics of
+// the page + combine pair (listed pages are summed now, the others are combined
+// from the records `scratch` holds). The list the reference's engine builds
+// (src/engine.cpp:93-103: rows ascending, each row's pages 0 .. last ascending)
+// puts row j's items at offset sum_{i<j} pages_i; the workgroup computes that
+// offset from row_pos and checks its row's stretch of the list. When it matches
+// (every page listed) the records stay in LDS and scratch is not touched.
+// Otherwise the workgroup scans the whole list for its row, sums the listed
+// pages, reads the unlisted pages' records from scratch and stores the records
+// it summed there, as k_attn_page would.
+constexpr int kListMaxPages = 320;  // pages a LIST workgroup tracks (the LDS bound is lower)
+
+template <int D, int NWV, bool LIST>
 __global__ __launch_bounds__(64 * NWV) void k_attn_fused(StrideAttentionParams p, int page_shift) {
   constexpr int kEl = 8;                        // bf16 elements per 16-byte piece
   constexpr int kPer = kAttnPage * D / kEl / 64;  // V pieces per lane
@@ -368,18 +380,55 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_fused(StrideAttentionParams p
   extern __shared__ float recs[];  // [max_pages][RF], f[4][max_pages], then the row's KV page numbers
   __shared__ f32x4 w4[NWV][kAttnPage];
   __shared__ uint16_t vs[NWV][kAttnPage][D];
+  __shared__ uint32_t listed[LIST ? kListMaxPages / 32 : 1];
+  __shared__ int part[NWV];
   const int j = blockIdx.x / p.n_kv;
   const int g = blockIdx.x % p.n_kv;
   const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
   const int slot = p.row_slot[j];
   const int visible = p.row_pos[j] + 1;
   const int last = visible - 1;
-  const int pages = (last >> kAttnPageShift) + 1;
+  // A row must satisfy row_pos < max_pages * 64 (the caller sizes max_pages for
+  // its longest row); the clamp keeps a row past it inside this workgroup's LDS.
+  const int pages = min((last >> kAttnPageShift) + 1, p.max_pages);
   // The row's KV page numbers, read once: every K/V address below then comes
   // from LDS, so a page's loads never wait on a dependent page-table load.
   int32_t* btab = reinterpret_cast<int32_t*>(recs + p.max_pages * (RF + kHeadsPerGroup));
-  const int nblk = (last >> page_shift) + 1;
+  const int nblk = min((last >> page_shift) + 1, (p.max_pages * kAttnPage + (1 << page_shift) - 1) >> page_shift);
   for (int i = t; i < nblk; i += 64 * NWV) btab[i] = p.kv.table[static_cast<int64_t>(slot) * p.kv.max_blocks + i];
+  // LIST: does the item list hold row j's pages where the engine's list puts them?
+  bool whole = true;
+  if constexpr (LIST) {
+    int s = 0;
+    for (int i = t; i < j; i += 64 * NWV) s += (p.row_pos[i] >> kAttnPageShift) + 1;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
+    if (lane == 0) part[wave] = s;
+    __syncthreads();
+    int off = 0;
+#pragma unroll
+    for (int w = 0; w < NWV; ++w) off += part[w];
+    int ok = off + pages <= p.item_count;
+    for (int c = t; ok && c < pages; c += 64 * NWV)
+      ok = p.items[2 * (off + c)] == j && p.items[2 * (off + c) + 1] == c;
+    whole = __syncthreads_and(ok) != 0;
+    if (!whole) {
+      for (int i = t; i < kListMaxPages / 32; i += 64 * NWV) listed[i] = 0u;
+      __syncthreads();
+      for (int i = t; i < p.item_count; i += 64 * NWV) {
+        const int c = p.items[2 * i + 1];
+        if (p.items[2 * i] == j && c >= 0 && c < pages) atomicOr(&listed[c >> 5], 1u << (c & 31));
+      }
+      __syncthreads();
+      // unlisted pages: the records an earlier call left in scratch
+      const float* src = p.scratch + static_cast<int64_t>(j * p.n_kv + g) * p.max_pages * p.rec_floats;
+      for (int u = t; u < pages * RF; u += 64 * NWV) {
+        const int c = u / RF, e = u % RF;
+        if (!((listed[c >> 5] >> (c & 31)) & 1u)) recs[c * RF + e] = src[static_cast<int64_t>(c) * p.rec_floats + e];
+      }
+    }
+  }
+  auto is_listed = [&](int page) { return !LIST || whole || ((listed[page >> 5] >> (page & 31)) & 1u); };
   const uint16_t* kv_base = static_cast<const uint16_t*>(p.kv.arena) + p.layer * p.kv.layer_elems + g * p.kv.group_elems;
   auto kv_at = [&](int which, int pos) {
     return kv_base + btab[pos >> page_shift] * p.kv.block_elems + which * p.kv.which_elems +
@@ -410,7 +459,7 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_fused(StrideAttentionParams p
   if (wave < pages) fetch(wave);
   for (int it = 0; it < rounds; ++it) {
     const int page = it * NWV + wave;
-    const bool active = page < pages;
+    const bool active = page < pages && is_listed(page);
     const int p0 = page << kAttnPageShift;
     const int n = active ? min(visible - p0, kAttnPage) : 0;
     if (active) {
@@ -488,6 +537,15 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_fused(StrideAttentionParams p
     }
     __syncthreads();  // the staging buffers are reused by the next round
   }
+  if constexpr (LIST) {
+    if (!whole) {  // store the summed records, as the page kernel does
+      float* dst = p.scratch + static_cast<int64_t>(j * p.n_kv + g) * p.max_pages * p.rec_floats;
+      for (int u = t; u < pages * RF; u += 64 * NWV) {
+        const int c = u / RF, e = u % RF;
+        if ((listed[c >> 5] >> (c & 31)) & 1u) dst[static_cast<int64_t>(c) * p.rec_floats + e] = recs[c * RF + e];
+      }
+    }
+  }
   // Combine in ascending page order (k_attn_combine's expressions). Each page
   // factor is computed by its own thread; every thread derives the head maximum
   // with the same ascending loop, so all agree; each output thread then forms
@@ -552,21 +610,25 @@ static int combine(dim3 grid, size_t lds, hipStream_t st, const StrideAttentionP
   return launched("attention (combine)");
 }
 
-// One-kernel attention (item_count == -1); its static LDS (staging for up to
-// four waves) and the row's records share the 160 KiB.
+// One-kernel attention; its static LDS (staging for up to four waves) and the
+// row's records share the 160 KiB.
 template <int D, int NWV>
+constexpr size_t fused_static_lds() {
+  return NWV * 64 * 16 + NWV * 64 * D * 2 + kListMaxPages / 8 + 4 * NWV;
+}
+
+template <int D, int NWV, bool LIST>
 static int fused_nwv(dim3 grid, size_t lds, hipStream_t st, const StrideAttentionParams& p, int page_shift) {
-  constexpr size_t kStatic = NWV * 64 * 16 + NWV * 64 * D * 2;
-  if (lds + kStatic > kCombineLdsMax)
+  if (lds + fused_static_lds<D, NWV>() > kCombineLdsMax)
     return fail(STRIDE_TC_EINVAL, "tc_attention: max_pages too large for the one-kernel form (use an item list)");
   static size_t raised = 64 * 1024;
   if (lds > raised) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn_fused<D, NWV>),
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn_fused<D, NWV, LIST>),
                                              hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
     if (e != hipSuccess) return fail(static_cast<int>(e), std::string("tc_attention: raising the LDS limit failed: ") + hipGetErrorString(e));
     raised = lds;
   }
-  hipLaunchKernelGGL((k_attn_fused<D, NWV>), grid, dim3(64 * NWV), lds, st, p, page_shift);
+  hipLaunchKernelGGL((k_attn_fused<D, NWV, LIST>), grid, dim3(64 * NWV), lds, st, p, page_shift);
   return launched("attention (one kernel)");
 }
 
@@ -575,11 +637,23 @@ static int fused_nwv(dim3 grid, size_t lds, hipStream_t st, const StrideAttentio
 // workgroups (batch 128, 1024 of them) two waves per workgroup (three rounds of
 // pages) measured best (30.9 us against 32.4 with three and 33+ with four); with
 // fewer (batch 64) four waves finish a row sooner.
-template <int D>
+template <int D, bool LIST>
 static int fused(dim3 grid, size_t lds, hipStream_t st, const StrideAttentionParams& p, int page_shift) {
-  if (grid.x >= 768) return fused_nwv<D, 2>(grid, lds, st, p, page_shift);
-  return fused_nwv<D, 4>(grid, lds, st, p, page_shift);
+  if (grid.x >= 768) return fused_nwv<D, 2, LIST>(grid, lds, st, p, page_shift);
+  return fused_nwv<D, 4, LIST>(grid, lds, st, p, page_shift);
 }
+
+// Does the one-kernel form serve a call with this dynamic LDS? (4 waves: the
+// larger static staging.)
+template <int D>
+static bool fused_fits(size_t lds) {
+  return lds + fused_static_lds<D, 4>() <= kCombineLdsMax;
+}
+
+// Item-list calls run the one-kernel form (which checks the list on the device)
+// for up to this many rows: each workgroup sums the page counts of the rows
+// before its own to find its stretch of the list, which grows with the row count.
+constexpr int kListFusedMaxRows = 512;
 
 static int launched(const char* what) {
   const hipError_t e = hipGetLastError();
@@ -652,14 +726,20 @@ static int attention(const StrideAttentionParams* p, void* stream, const char* n
   if (p->l.rows == 0) return 0;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if constexpr (!kExact) {
+    // records and page factors, then the row's KV page numbers
+    const size_t blocks = (static_cast<size_t>(p->max_pages) * kAttnPage + page_tokens - 1) / page_tokens;
+    const size_t lds = static_cast<size_t>(p->max_pages) * (8 + 4 * D + kHeadsPerGroup) * sizeof(float) + blocks * 4;
+    const dim3 grid(p->l.rows * p->n_kv);
     if (p->item_count == -1) {
-      // records and page factors, then the row's KV page numbers
-      const size_t blocks = (static_cast<size_t>(p->max_pages) * kAttnPage + page_tokens - 1) / page_tokens;
-      const size_t lds = static_cast<size_t>(p->max_pages) * (8 + 4 * D + kHeadsPerGroup) * sizeof(float) + blocks * 4;
-      const dim3 grid(p->l.rows * p->n_kv);
-      if (D == 32) return fused<32>(grid, lds, st, *p, page_shift);
-      if (D == 64) return fused<64>(grid, lds, st, *p, page_shift);
-      return fused<128>(grid, lds, st, *p, page_shift);
+      if (D == 32) return fused<32, false>(grid, lds, st, *p, page_shift);
+      if (D == 64) return fused<64, false>(grid, lds, st, *p, page_shift);
+      return fused<128, false>(grid, lds, st, *p, page_shift);
+    }
+    const bool fits = D == 32 ? fused_fits<32>(lds) : (D == 64 ? fused_fits<64>(lds) : fused_fits<128>(lds));
+    if (fits && p->max_pages <= kListMaxPages && p->l.rows <= kListFusedMaxRows) {
+      if (D == 32) return fused<32, true>(grid, lds, st, *p, page_shift);
+      if (D == 64) return fused<64, true>(grid, lds, st, *p, page_shift);
+      return fused<128, true>(grid, lds, st, *p, page_shift);
     }
   }
   using KvT = typename std::conditional<kExact, float, uint16_t>::type;

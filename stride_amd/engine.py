@@ -77,7 +77,7 @@ class Engine:
     """One model, a paged bf16 KV cache and the step buffers for up to max_rows rows."""
 
     def __init__(self, weights: Weights, slots: int, max_ctx: int, max_rows: int, page_tokens: int = 16,
-                 shuffle_seed: int = 0, attention_one_kernel: bool = True):
+                 shuffle_seed: int = 0, attention_one_kernel: bool = False):
         self.w = weights
         cfg = self.cfg = weights.cfg
         dev = self.dev = weights.embed.device
@@ -88,10 +88,14 @@ class Engine:
             raise ValueError(f"max_ctx {max_ctx} exceeds the RoPE table's {rope_positions} positions "
                              "(the QKV epilogue reads rope[pos] for every pos < max_ctx)")
         self.max_rows = max_rows
-        # every step lists every page of every row, so attention can run pages and
-        # combine as one kernel (item_count = -1); False keeps the item list
-        self.one_kernel = attention_one_kernel
         self.max_pages = (max_ctx + 63) // 64
+        # Every step passes the reference's item list (every page of every row),
+        # and the library runs pages and combine as one kernel when the records
+        # fit its LDS, else the page + combine pair. attention_one_kernel = True
+        # passes item_count = -1 instead (the same kernel without the list check),
+        # which only the LDS-fitting sizes accept, so it is dropped otherwise.
+        self.one_kernel = attention_one_kernel and harness.attention_one_kernel_fits(
+            self.max_pages, cfg.head_dim, page_tokens)
         lt = (max_rows + 15) // 16
         H, D = cfg.hidden, cfg.head_dim
         self.kv = harness.PagedKv.create(slots, max_ctx, cfg.kv_heads, D, cfg.layers, page_tokens, dev,

@@ -189,12 +189,22 @@ def compact(in_tiles, lm_rows, out_tiles=None):
     return out_tiles
 
 
+def attention_one_kernel_fits(max_pages: int, head_dim: int, page_tokens: int) -> bool:
+    """Whether tc_attention's one-kernel form serves rows of up to max_pages
+    64-position pages (the library's LDS budget: the records and page factors,
+    the row's KV page numbers and the staging of four waves within 159 KiB)."""
+    blocks = (max_pages * 64 + page_tokens - 1) // page_tokens
+    dynamic = max_pages * (8 + 4 * head_dim + 4) * 4 + blocks * 4
+    static = 4 * 64 * 16 + 4 * 64 * head_dim * 2 + 320 // 8 + 4 * 4
+    return dynamic + static <= 159 * 1024
+
+
 def attention(q, kv: PagedKv, row_slot, row_pos, n_kv: int, head_dim: int, scale: float, layer: int = 0,
               max_pages: int = 32, out_tiles=None, items=None, scratch=None, one_kernel: bool = False):
-    """tc_attention over every page of every row (as the engine's item list,
-    src/engine.cpp:93-103). q: [rows][n_kv*4*head_dim] fp32. Returns bf16 x tiles.
-    one_kernel: pass item_count = -1 (every page of every row), which runs pages
-    and combine in one kernel with the records in LDS (no item list, no scratch)."""
+    """tc_attention over the (row, page) list `items` (default: every page of every
+    row, the engine's list, src/engine.cpp:93-103). q: [rows][n_kv*4*head_dim] fp32.
+    Returns bf16 x tiles. one_kernel: pass item_count = -1 instead (every page of
+    every row, no item list, no scratch)."""
     rows = int(q.shape[0])
     cols = n_kv * 4 * head_dim
     dev = q.device

@@ -98,7 +98,9 @@ def test_compact():
 @pytest.mark.parametrize("page_tokens,n_kv,hd,cap,m", [(16, 8, 64, 320, 21), (64, 8, 64, 320, 21),
                                                         (16, 2, 128, 2048, 3), (32, 1, 32, 200, 9),
                                                         (16, 8, 64, 512, 130), (16, 1, 64, 7360, 2),
-                                                        (16, 1, 128, 2816, 2)])
+                                                        (16, 1, 128, 2816, 2),
+                                                        # past 512 rows item lists run the page + combine pair
+                                                        (16, 2, 64, 200, 600)])
 def test_attention(exact, page_tokens, n_kv, hd, cap, m):
     say("tc_attention page_tokens", page_tokens, "n_kv", n_kv, "hd", hd, "cap", cap, "m", m)
     rng = np.random.default_rng(5 + page_tokens + hd)
@@ -125,6 +127,55 @@ def test_attention(exact, page_tokens, n_kv, hd, cap, m):
                             one_kernel=True)
     got1 = layout.untile_lanes(one, m).cpu().numpy().view(np.uint16)
     assert np.array_equal(got1, want), f"one kernel: {(got1 != want).sum()} mismatches"
+
+
+def test_attention_item_lists(exact):
+    """The item-list semantics of the page + combine pair (src/engine.cpp:93-103,
+    src/kernels_tc.cu:668-679) hold for any list: the engine's own list (checked on
+    the device, one kernel), the same items shuffled, and partial lists whose
+    unlisted pages are combined from the records left in scratch. The one-kernel
+    form (max_pages 44 fits its LDS at head_dim 128) and the pair (max_pages 60
+    does not) agree bit for bit on a partial list."""
+    n_kv, hd, cap, m, page_tokens = 2, 128, 2816, 5, 16
+    rng = np.random.default_rng(21)
+    slots = 5
+    q = rng.standard_normal((m, n_kv * 4, hd)).astype(np.float32)
+    k = bf16_bits(rng.standard_normal((slots, n_kv, cap, hd)))
+    v = bf16_bits(rng.standard_normal((slots, n_kv, cap, hd)))
+    slot = rng.permutation(slots).astype(np.int32)
+    pos = np.array([cap - 1, 0, 700, 64, 1500], np.int32)
+    kv = harness.PagedKv.create(slots, cap, n_kv, hd, 1, page_tokens, DEV, shuffle_seed=4)
+    kv.fill_dense(0, 0, torch.from_numpy(k.view(np.int16)))
+    kv.fill_dense(0, 1, torch.from_numpy(v.view(np.int16)))
+    scale = hd ** -0.5
+    want = exact.tc_attention(q, k, v, slot, pos, scale)
+    qd, sd, pd = torch.from_numpy(q.reshape(m, -1)).to(DEV), torch.from_numpy(slot).to(DEV), torch.from_numpy(pos).to(DEV)
+    full = [(j, pg) for j in range(m) for pg in range((int(pos[j]) >> 6) + 1)]
+
+    def run(items, max_pages, scratch):
+        it = torch.tensor(items, dtype=torch.int32, device=DEV).reshape(-1)
+        out = harness.attention(qd, kv, sd, pd, n_kv, hd, scale, layer=0, max_pages=max_pages, items=it,
+                                scratch=scratch)
+        return layout.untile_lanes(out, m).cpu().numpy().view(np.uint16)
+
+    rec = 4 * hd + 8
+    scratch = lambda mp: torch.zeros(m * n_kv * mp * rec, dtype=torch.float32, device=DEV)
+    s44 = scratch(44)
+    say("tc_attention item list: engine order")
+    assert np.array_equal(run(full, 44, s44), want)
+    assert int(torch.count_nonzero(s44)) == 0  # whole rows keep their records in LDS
+    say("tc_attention item list: shuffled")
+    shuffled = [full[i] for i in rng.permutation(len(full))]
+    assert np.array_equal(run(shuffled, 44, s44), want)
+    say("tc_attention item list: last pages only, earlier records from scratch")
+    last = [(j, int(pos[j]) >> 6) for j in range(m)]
+    assert np.array_equal(run(last, 44, s44), want)
+    say("tc_attention item list: partial list over empty scratch, one kernel vs pair")
+    got44 = run(last[::2], 44, scratch(44))
+    got60 = run(last[::2], 60, scratch(60))
+    assert np.array_equal(got44, got60)
+    multi = [j for j in range(m) if pos[j] >= 64]
+    assert not np.array_equal(got44[multi], want[multi])
 
 
 def test_attention_rejects_bad_arguments():
