@@ -285,12 +285,14 @@ def cpu_threads_default():
     return max(1, min(len(os.sched_getaffinity(0)), share))
 
 
-def cpu_baseline(seconds, threads, batches=(128, 1)):
+def cpu_baseline(seconds, threads, batches=(128, 1), prefill=(290, 1024)):
     """The reference's exact path (oracle/_ref: its src/kernels.cu compiled as C++)
     on this host: one decode step's GEMM set at each batch in `batches`, sampled
     as one layer's QKV, O, gate+up and down GEMMs plus the LM head (the config-2
-    and config-3 shapes), with the layer time scaled to 16 layers. `value` is the
-    first batch's (the benchmark's M = 128) tok/s."""
+    and config-3 shapes), with the layer time scaled to 16 layers; the same five
+    GEMMs once each at the prefill row counts in `prefill` (config 4); and config 1
+    (one projection, M = 1, N = K = 2048). `value` is the first batch's (the
+    benchmark's M = 128) tok/s."""
     import ctypes as C
 
     import numpy as np
@@ -339,6 +341,27 @@ def cpu_baseline(seconds, threads, batches=(128, 1)):
             "per_gemm_ms": {k: round(v * 1e3, 3) for k, v in t.items()},
             "per_gemm_GB/s": {nm: round((2 * n * k + 4 * m * (k + n)) / t[nm] / 1e9, 2) for nm, n, k in dims},
             "per_gemm_GFLOP/s": {nm: round(2 * m * n * k / t[nm] / 1e9, 2) for nm, n, k in dims}}
+    def once(w, n, k, m):
+        x = rng.standard_normal((m, k), dtype=np.float32)
+        if lib is not None:
+            return lib.ref_bench_gemm(w, n, k, x, m, 1)
+        t0 = time.perf_counter()
+        ex.gemm(w, x)
+        return time.perf_counter() - t0
+
+    w1 = wts(HIDDEN, HIDDEN)
+    sec1 = min(once(w1, HIDDEN, HIDDEN, 1) for _ in range(5))
+    config1 = {"M": 1, "N": HIDDEN, "K": HIDDEN, "ms": round(sec1 * 1e3, 4),
+               "GB/s": round((2 * HIDDEN * HIDDEN + 4 * (2 * HIDDEN)) / sec1 / 1e9, 2),
+               "GFLOP/s": round(2 * HIDDEN * HIDDEN / sec1 / 1e9, 2), "repetitions": 5, "statistic": "min"}
+    pre = {}
+    for name, n, k in dims:
+        w = wts(n, k)
+        for m in prefill:
+            sec = once(w, n, k, m)
+            pre.setdefault(str(m), {})[name] = {"ms": round(sec * 1e3, 2),
+                                                "GFLOP/s": round(2 * m * n * k / sec / 1e9, 1)}
+        del w
     m0 = batches[0]
     out = {"value": per_batch[m0]["tok_s"], "unit": "tok/s", "cores": threads, "kind": kind,
            "sample": f"exact path (k_lm_full order, all fmaf chains) at batch {m0}: one layer's QKV/O/gate+up/down "
@@ -346,6 +369,8 @@ def cpu_baseline(seconds, threads, batches=(128, 1)):
                      f"{threads}", "seconds_per_step": per_batch[m0]["seconds_per_step"]}
     out.update(host_info())
     out["batches"] = {str(m): v for m, v in per_batch.items()}
+    out["config1"] = config1
+    out["prefill"] = {"repetitions": 1, "per_gemm": pre}
     return out
 
 
@@ -356,7 +381,7 @@ def cpu_baseline_single_core(seconds):
     import subprocess
 
     env = dict(os.environ, STRIDE_CPU_THREADS="1")
-    code = f"import json, bench; print(json.dumps(bench.cpu_baseline({seconds!r}, 1, (1,))))"
+    code = f"import json, bench; print(json.dumps(bench.cpu_baseline({seconds!r}, 1, (1,), ())))"
     try:
         r = subprocess.run([sys.executable, "-c", code], cwd=ROOT, env=env, capture_output=True, text=True,
                            timeout=120 + 4 * seconds)

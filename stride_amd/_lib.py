@@ -185,7 +185,6 @@ EXPORTS = (
     "stride_tc_last_error",
     "stride_tc_version",
     "stride_tc_set_stream_config",
-    "stride_tc_set_split_rule",
     "stride_tc_stream_config_count",
     "stride_tc_pipe_config_count",
     "stride_tc_dec_config_count",
@@ -258,8 +257,6 @@ def load(path: str = LIB_PATH) -> C.CDLL:
         fn.restype = C.c_int
     lib.stride_tc_set_stream_config.argtypes = [C.c_int32]
     lib.stride_tc_set_stream_config.restype = C.c_int
-    lib.stride_tc_set_split_rule.argtypes = [C.c_int32]
-    lib.stride_tc_set_split_rule.restype = C.c_int
     lib.stride_tc_stream_config_count.argtypes = []
     lib.stride_tc_stream_config_count.restype = C.c_int
     lib.stride_tc_pipe_config_count.argtypes = []
@@ -321,12 +318,6 @@ def stream_configs():
 def set_stream_config(index: int) -> None:
     """Force a decode-regime configuration (-1 = automatic); results never change."""
     check(load().stride_tc_set_stream_config(index))
-
-
-def set_split_rule(splits: int) -> None:
-    """Split count of matrices with N <= 4096 (default 4). Changes the bits: for
-    split-rule experiments only."""
-    check(load().stride_tc_set_split_rule(splits))
 
 
 def last_stream_config() -> int:

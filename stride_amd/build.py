@@ -21,9 +21,12 @@ CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_obj")
 SOURCES = [os.path.join(CSRC, f) for f in ("tc_gemm.hip", "tc_gemm_mlp13.hip", "tc_gemm_qkv.hip", "tc_gemm_lm_full.hip",
                                             "tc_gemm_lm_greedy.hip", "tc_aux.hip", "exact.hip")]
+# (source, object name, extra flags): the entry points, then each epilogue's
+# configuration table of each kernel family in an object of its own.
+UNITS = [(s, os.path.basename(s) + ".o", []) for s in SOURCES] + [
+    (os.path.join(CSRC, "tc_gemm_inst.hip"), f"inst_{epi}_{fam}.o", [f"-DSTRIDE_TC_EPI={epi}", f"-DSTRIDE_TC_FAMILY={fam}"])
+    for epi in ("EpiResidual", "EpiLogits", "EpiGateUp", "EpiArgmax", "EpiQkv") for fam in (0, 1, 2)]
 OUT = os.path.join(HERE, "libstride_tc.so")
-PROBE_SOURCES = [os.path.join(CSRC, "probe.hip")]
-PROBE_OUT = os.path.join(HERE, "libstride_probe.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
     "-O3", "--offload-arch=gfx950", "-std=c++17", "-fPIC",
@@ -46,25 +49,25 @@ def _deps_mtime(src: str) -> float:
     return max(os.path.getmtime(f) for f in files)
 
 
-def _link(out: str, sources, verbose: bool, incremental: bool) -> None:
+def _link(out: str, units, verbose: bool, incremental: bool) -> None:
     os.makedirs(OBJ, exist_ok=True)
-    objs = [os.path.join(OBJ, os.path.basename(s) + ".o") for s in sources]
-    def compile_one(src_obj):
-        src, obj = src_obj
+    objs = [os.path.join(OBJ, name) for _, name, _ in units]
+
+    def compile_one(unit_obj):
+        (src, _, extra), obj = unit_obj
         if incremental and os.path.exists(obj) and os.path.getmtime(obj) > _deps_mtime(src):
             return
-        _run([HIPCC, *FLAGS, "-c", "-o", obj, src], os.path.basename(src), verbose)
+        _run([HIPCC, *FLAGS, *extra, "-c", "-o", obj, src], os.path.basename(obj), verbose)
 
-    with ThreadPoolExecutor(max_workers=len(sources)) as ex:
-        list(ex.map(compile_one, zip(sources, objs)))
+    workers = max(1, min(len(units), os.cpu_count() or 1))
+    with ThreadPoolExecutor(max_workers=workers) as ex:
+        list(ex.map(compile_one, zip(units, objs)))
     _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", out, *objs], os.path.basename(out), verbose)
 
 
 def build(verbose: bool = False, incremental: bool = False) -> str:
-    """Builds libstride_tc.so (the GEMM library) and libstride_probe.so (the
-    methodology probes)."""
-    _link(OUT, SOURCES, verbose, incremental)
-    _link(PROBE_OUT, PROBE_SOURCES, verbose, incremental)
+    """Builds libstride_tc.so (the GEMM library)."""
+    _link(OUT, UNITS, verbose, incremental)
     return OUT
 
 

@@ -89,6 +89,16 @@ ScratchSet scratch_for(hipStream_t st) {
     pick = 0;
     for (int i = 1; i < kScratchSets; ++i)
       if (d.last_use[i] < d.last_use[pick]) pick = i;
+#ifdef STRIDE_TC_DEBUG
+    // A fifth stream takes over the least recently used set. In debug builds that
+    // is refused while the set's previous stream still has work queued (which
+    // would race on the partials and counters). The previous stream must still
+    // exist, which release builds cannot assume, hence no such check there.
+    if (hipStreamQuery(d.owner[pick]) == hipErrorNotReady) {
+      fail(STRIDE_TC_EINVAL, "scratch set of another stream is still in use (more than four streams in flight)");
+      return {};
+    }
+#endif
   }
   d.used[pick] = true;
   d.owner[pick] = st;
@@ -97,7 +107,6 @@ ScratchSet scratch_for(hipStream_t st) {
 }
 
 int g_forced_cfg = -1;
-int g_split_few = 4;
 int g_forced_dec = -1;
 int g_forced_pipe = -1;
 int g_last_cfg = -1;
@@ -212,13 +221,6 @@ int stride_tc_set_stream_config(int32_t index) {
   if (index < -1 || index >= kNumDecodeCfgs) return fail(STRIDE_TC_EINVAL, "config index out of range");
   g_forced_cfg = index;
   g_forced_pipe = g_forced_dec = -1;
-  return 0;
-}
-
-int stride_tc_set_split_rule(int32_t splits) {
-  if (splits != 1 && splits != 2 && splits != 4 && splits != 8 && splits != 16)
-    return fail(STRIDE_TC_EINVAL, "split rule: splits must be 1, 2, 4, 8 or 16");
-  g_split_few = splits;
   return 0;
 }
 

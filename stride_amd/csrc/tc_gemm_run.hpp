@@ -38,11 +38,19 @@ int fail(int code, const std::string& msg);
 // single split lets the prefill kernels keep one accumulator per tile instead
 // of a split partial and a running sum. S is then capped by the chunk count and
 // halved until it divides it.
-extern int g_split_few;  // splits of matrices with N <= 4096 (tuning hook; default 8)
+// The split count of matrices with N <= 4096 is a constant of the build (4). A
+// library built with another STRIDE_TC_SPLIT_FEW computes other bits, so it is a
+// different library; nothing at run time can change it.
+#ifndef STRIDE_TC_SPLIT_FEW
+#define STRIDE_TC_SPLIT_FEW 4
+#endif
+constexpr int kSplitFew = STRIDE_TC_SPLIT_FEW;
+static_assert(kSplitFew == 1 || kSplitFew == 2 || kSplitFew == 4 || kSplitFew == 8 || kSplitFew == 16,
+              "split count of the few-row matrices: 1, 2, 4, 8 or 16");
 
 inline int split_count(int n, int k) {
   const int chunks = k / kChunkCols;
-  int s = n <= 4096 ? g_split_few : 1;
+  int s = n <= 4096 ? kSplitFew : 1;
   if (s > chunks) s = chunks;
   while (s > 1 && chunks % s != 0) s >>= 1;
   return s < 1 ? 1 : s;
@@ -647,6 +655,20 @@ inline Pick pick_large(const Geometry& g, int T, int smax, int mats, int per) {
   return {1, 2};
 }
 
+// The configuration tables are instantiated once per epilogue and kernel family
+// in tc_gemm_inst.hip (compiled once per pair, so the library builds in
+// parallel); the entry points' translation units only declare them.
+#define STRIDE_TC_EXTERN_TABLES(E)                                                                   \
+  extern template void launch_decode_cfg<E>(int, const Geometry&, const E::Out&, hipStream_t);      \
+  extern template void launch_dec_cfg<E>(int, const Geometry&, const E::Out&, hipStream_t);         \
+  extern template void launch_pipe_cfg<E>(int, const Geometry&, const E::Out&, int, hipStream_t);
+STRIDE_TC_EXTERN_TABLES(EpiResidual)
+STRIDE_TC_EXTERN_TABLES(EpiLogits)
+STRIDE_TC_EXTERN_TABLES(EpiGateUp)
+STRIDE_TC_EXTERN_TABLES(EpiArgmax)
+STRIDE_TC_EXTERN_TABLES(EpiQkv)
+#undef STRIDE_TC_EXTERN_TABLES
+
 template <class Epi>
 int run(Geometry g, const typename Epi::Out& o_in, hipStream_t st) {
   if (g.rows == 0) return 0;
@@ -705,7 +727,10 @@ int run(Geometry g, const typename Epi::Out& o_in, hipStream_t st) {
     o.cand = nullptr;
     if (kind != 2 && g.nseg == 1) {
       nrb = (g.seg[0].row_tiles + rows_per_block - 1) / rows_per_block;
-      if (static_cast<int64_t>(nrb) * g.rows <= kCandSlots) o.cand = scratch_for(st).scratch;
+      if (static_cast<int64_t>(nrb) * g.rows <= kCandSlots) {
+        o.cand = scratch_for(st).scratch;
+        if (!o.cand) return fail(STRIDE_TC_EINVAL, "argmax scratch unavailable");
+      }
       if (!o.cand) nrb = 0;
       o.nrb = nrb;
     }

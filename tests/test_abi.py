@@ -114,20 +114,11 @@ def test_split_rule():
         tc.split_count(16, 24)
 
 
-def test_split_rule_hook():
-    """The split-rule tuning hook (experiments only: it changes the bits) takes 1, 2,
-    4, 8 or 16 splits for the few-row matrices and nothing else; gate/up and the LM
-    head keep one split."""
-    try:
-        for s in (1, 2, 8, 16):
-            _lib.set_split_rule(s)
-            assert tc.split_count(2048, 8192) == s
-            assert tc.split_count(8192, 2048) == 1
-        for bad in (0, 3, 32, -1):
-            with pytest.raises(_lib.StrideTcError):
-                _lib.set_split_rule(bad)
-    finally:
-        _lib.set_split_rule(4)
+def test_split_rule_has_no_runtime_hook():
+    """The split rule is a constant of the build: the library exports no call that
+    changes it, so the bits depend on the weight shape only."""
+    lib = _lib.load()
+    assert not hasattr(lib, "stride_tc_set_split_rule")
     assert tc.split_count(2048, 2048) == 4
 
 

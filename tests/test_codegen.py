@@ -85,9 +85,9 @@ def test_scanner_flags_unguarded_mfma():
     assert masked_mfmas(bad) and not masked_mfmas(good)
 
 
-@pytest.mark.parametrize("lib", ["libstride_tc.so", "libstride_probe.so"])
+@pytest.mark.parametrize("lib", ["stride_amd/libstride_tc.so", "tests/kat/libmfma_kat.so"])
 def test_no_mfma_under_exec_mask(lib):
-    path = os.path.join(PKG, lib)
+    path = os.path.join(os.path.dirname(PKG), lib)
     if not os.path.exists(path):
         pytest.skip(lib + " not built")
     if not os.path.exists(OBJDUMP):

@@ -1,4 +1,4 @@
-"""Methodology probes on the GPU.
+"""Hardware known-answer tests on the GPU (kernels in tests/kat/mfma_kat.hip).
 
 MFMA position invariance (the gfx950 counterpart of the reference's tc_probe Q1,
 tools/tc_probe.cu:106-139, reports/g3/tc_probe.txt:1): permuting the rows of A
@@ -8,11 +8,14 @@ bit. This is the hardware fact the whole batch-invariance design rests on: an
 output element's bits depend only on its own row, lane and K chunk, never on where
 in the tile that row or lane sits.
 """
-import numpy as np
+import os
+import sys
+
 import pytest
 import torch
 
-from stride_amd import probe
+sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "kat"))
+import kat  # noqa: E402
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
@@ -30,7 +33,7 @@ def test_mfma_position_invariance():
     b = torch.randn(tiles, 2, 16, 16, generator=g, device=DEV).to(torch.bfloat16)
     c = torch.randn(tiles, 16, 16, generator=g, device=DEV)
     out = torch.empty_like(c)
-    probe.mfma_tiles(a.view(torch.int16), b.view(torch.int16), c, out, stream())
+    kat.mfma_tiles(a.view(torch.int16), b.view(torch.int16), c, out, stream())
     # float64 reference: out[t][n][m] = c[t][n][m] + sum_k A[t][m][k] B[t][n][k]
     A = a.double().permute(0, 2, 1, 3).reshape(tiles, 16, 32)
     B = b.double().permute(0, 2, 1, 3).reshape(tiles, 16, 32)
@@ -43,22 +46,11 @@ def test_mfma_position_invariance():
     bp = b[t, :, lp].permute(0, 2, 1, 3).contiguous()          # lanes permuted
     cp = c[t, lp][t[:, :, None], torch.arange(16, device=DEV)[None, :, None], rp[:, None, :]].contiguous()
     outp = torch.empty_like(c)
-    probe.mfma_tiles(ap.view(torch.int16), bp.view(torch.int16), cp, outp, stream())
+    kat.mfma_tiles(ap.view(torch.int16), bp.view(torch.int16), cp, outp, stream())
     expect = out[t, lp][t[:, :, None], torch.arange(16, device=DEV)[None, :, None], rp[:, None, :]]
     same = int((outp.view(torch.int32) == expect.contiguous().view(torch.int32)).sum())
     print(f"MFMA row/lane permutation: {same} / {outp.numel()} elements bit-identical", flush=True)
     assert same == outp.numel()
-
-
-def test_read_probe_checksum():
-    n = 1 << 22  # 16 MiB of int32
-    buf = torch.randint(-2**31, 2**31 - 1, (n,), dtype=torch.int32, device=DEV)
-    want = np.bitwise_xor.reduce(buf.cpu().numpy().view(np.uint32))
-    for unroll in (1, 4, 8, 16):
-        out = torch.zeros(1024, dtype=torch.int32, device=DEV)
-        probe.read(buf, out, 1024, unroll, stream())
-        got = np.bitwise_xor.reduce(out.cpu().numpy().view(np.uint32))
-        assert got == want, unroll
 
 
 def test_mfma_shapes_equivalent():
@@ -77,7 +69,7 @@ def test_mfma_shapes_equivalent():
         a, b = a.to(torch.bfloat16), b.to(torch.bfloat16)
         c0 = torch.randn(cases, 32, 32, generator=g, device=DEV)
         o16, o32 = torch.empty_like(c0), torch.empty_like(c0)
-        probe.mfma_equiv(a.view(torch.int16), b.view(torch.int16), c0, o16, o32, chunks, stream())
+        kat.mfma_equiv(a.view(torch.int16), b.view(torch.int16), c0, o16, o32, chunks, stream())
         torch.cuda.synchronize()
         ref = c0.double() + torch.einsum("tmk,tnk->tmn", a.double(), b.double())
         assert torch.allclose(o16.double(), ref, rtol=1e-3, atol=1e-3 * ref.abs().max().item())

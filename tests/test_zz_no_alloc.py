@@ -24,6 +24,35 @@ def case(seed, n, k, m):
     return w, x
 
 
+def test_noalloc_under_graph_capture():
+    """The entry point's first call in the process happens inside a HIP graph
+    capture (it resolves the scratch address there); each replay, with eager
+    launches of the workspace entry point and synchronizations in between, gives
+    the eager bits."""
+    n, k, m = 2048, 2048, 40
+    say("f32x noalloc under capture: n", n, "k", k, "m", m)
+    w, x = case(4, n, k, m)
+    want = harness.gemm_f32x(w, x, m)
+    torch.cuda.synchronize()
+    got = torch.full_like(want, float("nan"))
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g):
+            harness.gemm_f32x_noalloc(w, x, m, got)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    for i in range(3):
+        got.fill_(float("nan"))
+        w2, x2 = case(10 + i, 1024, 4096, 17 + i)
+        harness.gemm_f32x(w2, x2, 17 + i)  # eager work on the scratch sets between replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(layout.untile_lanes(got, m).view(torch.int32), layout.untile_lanes(want, m).view(torch.int32)), i
+
+
 def test_noalloc_matches_workspace_entry_point_twice():
     for seed, n, k, m in ((1, 2048, 8192, 200), (2, 3072, 2048, 37)):
         say("f32x noalloc: n", n, "k", k, "m", m)
