@@ -14,6 +14,7 @@ its staging ring, NS stages x (mats*WM*WRT + WN*WLT) tiles x KC chunks x 1 KiB.
 Anything more is a private copy the compiler moved into LDS (a local struct
 indexed at run time), which costs LDS capacity and an LDS round trip per use.
 """
+import functools
 import os
 import re
 import struct
@@ -28,23 +29,53 @@ OBJDUMP = "/opt/rocm/llvm/bin/llvm-objdump"
 MAGIC = b"__CLANG_OFFLOAD_BUNDLE__"
 
 
-def code_object(lib_path: str) -> bytes:
-    """The gfx950 code object from the offload bundle embedded in a hipcc-built .so
-    (bundle layout: magic, u64 count, then per entry u64 offset, u64 size, u64
-    triple length, triple)."""
+def code_objects(lib_path: str):
+    """The gfx950 code objects of every offload bundle embedded in a hipcc-built
+    .so (one per translation unit; bundle layout: magic, u64 count, then per
+    entry u64 offset, u64 size, u64 triple length, triple)."""
     data = open(lib_path, "rb").read()
+    out = []
     base = data.find(MAGIC)
-    assert base >= 0, "no offload bundle in " + lib_path
-    (count,) = struct.unpack_from("<Q", data, base + len(MAGIC))
-    p = base + len(MAGIC) + 8
-    for _ in range(count):
-        off, size, tlen = struct.unpack_from("<QQQ", data, p)
-        p += 24
-        triple = data[p:p + tlen].decode()
-        p += tlen
-        if "gfx950" in triple:
-            return data[base + off:base + off + size]
-    raise AssertionError("no gfx950 code object in " + lib_path)
+    while base >= 0:
+        (count,) = struct.unpack_from("<Q", data, base + len(MAGIC))
+        p = base + len(MAGIC) + 8
+        for _ in range(count):
+            off, size, tlen = struct.unpack_from("<QQQ", data, p)
+            p += 24
+            triple = data[p:p + tlen].decode(errors="replace")
+            p += tlen
+            if "gfx950" in triple:
+                out.append(data[base + off:base + off + size])
+        base = data.find(MAGIC, base + len(MAGIC))
+    assert out, "no gfx950 code object in " + lib_path
+    return out
+
+
+@functools.lru_cache(maxsize=None)
+def disassemble(lib_path: str) -> str:
+    """gfx950 disassembly of every code object in the library."""
+    parts = []
+    with tempfile.TemporaryDirectory() as d:
+        for i, obj in enumerate(code_objects(lib_path)):
+            co = os.path.join(d, f"k{i}.co")
+            open(co, "wb").write(obj)
+            parts.append(subprocess.run([OBJDUMP, "-d", "--mcpu=gfx950", co], capture_output=True, text=True,
+                                        check=True).stdout)
+    return "\n".join(parts)
+
+
+def functions(disasm: str):
+    """{function label: [instruction lines]} of a disassembly."""
+    out, fn = {}, None
+    for line in disasm.splitlines():
+        s = line.strip()
+        m = re.match(r"^[0-9a-f]+ <(.+)>:$", s)
+        if m:
+            fn = m.group(1)
+            out[fn] = []
+        elif fn and s:
+            out[fn].append(s)
+    return out
 
 
 NARROW = ("s_and_saveexec", "s_andn2_saveexec", "s_or_saveexec", "s_xor_saveexec", "s_and_b64 exec",
@@ -92,10 +123,7 @@ def test_no_mfma_under_exec_mask(lib):
         pytest.skip(lib + " not built")
     if not os.path.exists(OBJDUMP):
         pytest.skip("llvm-objdump not available")
-    with tempfile.TemporaryDirectory() as d:
-        co = os.path.join(d, "k.co")
-        open(co, "wb").write(code_object(path))
-        dis = subprocess.run([OBJDUMP, "-d", "--mcpu=gfx950", co], capture_output=True, text=True, check=True).stdout
+    dis = disassemble(path)
     assert "v_mfma" in dis
     bad = masked_mfmas(dis)
     assert not bad, f"{len(bad)} MFMAs under an exec mask, first in {bad[0][0]}"
@@ -121,10 +149,12 @@ def test_pipe_lds_is_exactly_the_ring():
         pytest.skip("libstride_tc.so not built")
     if not os.path.exists(OBJDUMP):
         pytest.skip("llvm tools not available")
+    kernels = []
     with tempfile.TemporaryDirectory() as d:
-        co = os.path.join(d, "k.co")
-        open(co, "wb").write(code_object(path))
-        kernels = kernel_lds(co)
+        for i, obj in enumerate(code_objects(path)):
+            co = os.path.join(d, f"k{i}.co")
+            open(co, "wb").write(obj)
+            kernels += kernel_lds(co)
     seen = 0
     for name, grp in kernels:
         m = re.search(r"k_pipe(?:32)?INS_\d+(\w+?)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELb(\d)", name)
@@ -134,4 +164,36 @@ def test_pipe_lds_is_exactly_the_ring():
         mats = 2 if m.group(1) == "EpiGateUp" else 1
         assert grp == ns * (mats * wm * wrt + wn * wlt) * kc * 1024, f"{name}: {grp} bytes of LDS"
         seen += 1
+    assert seen > 0
+
+
+def test_split_partials_travel_device_coherent():
+    """The one-split-per-workgroup kernels publish split partials with 16-byte
+    buffer stores and read them back with buffer loads, both with the sc1 cache
+    policy (coherent at device scope across XCDs), and every such store has
+    completed (s_waitcnt vmcnt(0)) before the workgroup's arrival atomic. The
+    fixed-order fold relies on exactly this code; a compiler that emitted the
+    accesses without sc1, or moved the atomic ahead of the wait, would break it
+    silently, so the built machine code is checked here."""
+    path = os.path.join(PKG, "libstride_tc.so")
+    if not os.path.exists(path):
+        pytest.skip("libstride_tc.so not built")
+    if not os.path.exists(OBJDUMP):
+        pytest.skip("llvm-objdump not available")
+    seen = 0
+    for name, ins in functions(disassemble(path)).items():
+        stores = [i for i, s in enumerate(ins) if s.startswith("buffer_store_dwordx4")]
+        if not stores:
+            continue
+        seen += 1
+        for s in ins:
+            if s.startswith(("buffer_store_dwordx4", "buffer_load_dwordx4")):
+                assert " sc1" in s, f"{name}: {s}"
+        atomics = [i for i, s in enumerate(ins) if s.startswith("global_atomic_add")]
+        assert atomics, f"{name}: partial stores but no arrival atomic"
+        for a in atomics:
+            before = [i for i in stores if i < a]
+            if before:
+                waits = [s for s in ins[before[-1]:a] if s.startswith("s_waitcnt") and "vmcnt(0)" in s]
+                assert waits, f"{name}: arrival atomic not after vmcnt(0)"
     assert seen > 0
