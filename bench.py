@@ -53,6 +53,9 @@ def parse():
                     help="run only the full decode step (for kernel profiles of it) and print its JSON")
     ap.add_argument("--engine", type=int, default=1,
                     help="also time one full decode step of the engine (0 to skip)")
+    ap.add_argument("--step-only", type=int, default=0,
+                    help="run only the replays of the step graph (no eager pass, no per-op timing; for kernel "
+                    "profiles of the step as it is measured) and print its time")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="also run one plain device copy of this size (calibrates FETCH_SIZE/WRITE_SIZE counters)")
     return ap.parse_args()
@@ -130,7 +133,6 @@ class Buffers:
         self.slots = torch.arange(m, dtype=torch.int32, device=dev)
         self.pos = torch.full((m,), 10, dtype=torch.int32, device=dev)
         self.best = harness.best_init(m, dev)
-        self.best0 = harness.best_init(m, dev)
 
 
 # Weights each op reads, and the least bytes one pass of a per-op timing graph reads.
@@ -154,7 +156,7 @@ def op_launch(name, W, b, li=0):
         return lambda: harness.gemm_residual(W["w2"], b.z, b.h, m)
     # best is re-initialised before every argmax, as the engine uploads {-inf, -1}
     # each step (reference src/engine.cpp:423-424); the reset is part of the op.
-    return lambda: (b.best.copy_(b.best0), harness.lm_greedy(W["lm"], b.x, m, VOCAB, best=b.best))
+    return lambda: (harness.best_reset(b.best), harness.lm_greedy(W["lm"], b.x, m, VOCAB, best=b.best))
 
 
 def rotated_ops(model, b, names):
@@ -498,6 +500,20 @@ def main():
     from stride_amd import harness
 
     step = [f for _, f in ops]
+
+    if a.step_only:
+        graph = capture(torch, step)
+        for _ in range(a.warmup):
+            graph.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(a.steps):
+            graph.replay()
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+        print(json.dumps({"step_only": True, "M": a.m, "steps": a.steps, "ms_per_step": round(dt / a.steps * 1e3, 4)}),
+              flush=True)
+        return
 
     # Eager (host-launched) rate, for reference.
     for _ in range(a.warmup):

@@ -108,7 +108,6 @@ class Engine:
         self.q = torch.zeros((max_rows, cfg.heads * D), dtype=torch.float32, device=dev)
         self.scratch = torch.zeros(max_rows * cfg.kv_heads * self.max_pages * (4 * D + 8), dtype=torch.float32,
                                    device=dev)
-        self.best_init = harness.best_init(max_rows, dev)
 
     def launch(self, n: int, slot, pos, tok, items, greedy=None, best=None) -> None:
         """Enqueue one step over n rows described by device tensors (row slots,
@@ -137,7 +136,7 @@ class Engine:
         if greedy is not None:
             harness.compact(self.x, greedy, out_tiles=self.lm_x)
             x = self.lm_x
-        best.copy_(self.best_init[:count])
+        harness.best_reset(best)
         harness.lm_greedy(w.lm, x, count, cfg.vocab, best=best)
 
     def device_rows(self, rows):
