@@ -56,6 +56,15 @@ def parse():
     ap.add_argument("--step-only", type=int, default=0,
                     help="run only the replays of the step graph (no eager pass, no per-op timing; for kernel "
                     "profiles of the step as it is measured) and print its time")
+    ap.add_argument("--summarize-trace", default="",
+                    help="print per-kernel launch counts and durations from a rocprofv3 kernel_trace.csv and exit")
+    ap.add_argument("--summarize-counters", default="",
+                    help="print the average value per dispatch of each counter per kernel from a rocprofv3 "
+                    "counter_collection.csv and exit")
+    ap.add_argument("--traffic-from", default="",
+                    help="FETCH_CSV,WRITE_CSV: print the HBM bytes per launch of each kernel from a rocprofv3 "
+                    "FETCH_SIZE run and a WRITE_SIZE run of this benchmark with --copy-calib-mib 512 (the JSON "
+                    "the roofline's traffic field reads) and exit")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="also run one plain device copy of this size (calibrates FETCH_SIZE/WRITE_SIZE counters)")
     return ap.parse_args()
@@ -264,6 +273,85 @@ def measured_traffic(op, m):
     return int(hits[0]) if len(hits) == 1 else None
 
 
+def short_kernel(name):
+    """Kernel name without namespaces, argument list or a leading `void`."""
+    import re
+
+    name = name.replace("stride_tc::", "")
+    name = re.sub(r"\(Geometry.*$", "", name)
+    return re.sub(r"^void ", "", name)[:140]
+
+
+def summarize_trace(path):
+    """calls / average / min / max / total duration (us) per kernel of a rocprofv3
+    kernel trace, largest total first."""
+    import csv
+    from collections import defaultdict
+
+    rows = defaultdict(list)
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            rows[short_kernel(r["Kernel_Name"])].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    lines = [f"{'kernel':<90} {'calls':>6} {'avg_us':>9} {'min_us':>9} {'max_us':>9} {'total_us':>11}"]
+    for n, d in sorted(rows.items(), key=lambda kv: -sum(kv[1])):
+        lines.append(f"{n[:90]:<90} {len(d):>6} {sum(d) / len(d):>9.2f} {min(d):>9.2f} {max(d):>9.2f} {sum(d):>11.1f}")
+    return "\n".join(lines)
+
+
+def summarize_counters(path):
+    """Average value per dispatch of each counter, per kernel (FETCH_SIZE and
+    WRITE_SIZE in KiB), from a rocprofv3 counter collection."""
+    import csv
+    from collections import defaultdict
+
+    vals = defaultdict(lambda: defaultdict(float))
+    disp = defaultdict(lambda: defaultdict(set))
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            n = short_kernel(r["Kernel_Name"])
+            vals[n][r["Counter_Name"]] += float(r["Counter_Value"])
+            disp[n][r["Counter_Name"]].add(r["Dispatch_Id"])
+    lines = [f"{'kernel':<90} {'counter':>28} {'dispatches':>10} {'avg_per_dispatch':>18}"]
+    for n in sorted(vals):
+        for c in sorted(vals[n]):
+            k = len(disp[n][c])
+            lines.append(f"{n[:90]:<90} {c:>28} {k:>10} {vals[n][c] / k:>18.1f}")
+    return "\n".join(lines)
+
+
+def traffic_from(fetch_csv, write_csv, calib_bytes=512 << 20):
+    """HBM bytes per launch by kernel: FETCH_SIZE and WRITE_SIZE (KiB per
+    dispatch, averaged over dispatches), each scaled by what the counter reads
+    for the plain copy (torch neg) of calib_bytes each way in the same run."""
+    import csv
+    from collections import defaultdict
+
+    def per_dispatch(path, counter):
+        vals, disp = defaultdict(float), defaultdict(set)
+        with open(path) as f:
+            for r in csv.DictReader(f):
+                if r["Counter_Name"] == counter:
+                    n = short_kernel(r["Kernel_Name"])
+                    vals[n] += float(r["Counter_Value"])
+                    disp[n].add(r["Dispatch_Id"])
+        return {n: vals[n] / len(disp[n]) for n in vals}
+
+    fetch, write = per_dispatch(fetch_csv, "FETCH_SIZE"), per_dispatch(write_csv, "WRITE_SIZE")
+    cal = [n for n in fetch if "neg_kernel" in n]
+    if len(cal) != 1 or cal[0] not in write:
+        raise SystemExit(f"bench.py: need exactly one calibration copy kernel in both runs, found {cal}")
+    fs, ws = calib_bytes / (fetch[cal[0]] * 1024.0), calib_bytes / (write[cal[0]] * 1024.0)
+    out = {"source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE --kernel-trace, one run each",
+           "calibration": {"kernel": cal[0], "bytes_each_way": calib_bytes, "fetch_scale": round(fs, 4),
+                           "write_scale": round(ws, 4)},
+           "kernels": {}}
+    for n in sorted(fetch):
+        if n != cal[0] and n in write and n.startswith("k_"):
+            fb, wb = fetch[n] * 1024.0 * fs, write[n] * 1024.0 * ws
+            out["kernels"][n] = {"fetch_bytes": int(fb), "write_bytes": int(wb), "hbm_bytes": int(fb + wb)}
+    return out
+
+
 def host_info():
     """Host cores (as os.cpu_count() reports them), the cores this process may run
     on, and the CPU model string."""
@@ -470,6 +558,16 @@ def main():
 
     from stride_amd import _lib
 
+    if a.summarize_trace:
+        print(summarize_trace(a.summarize_trace))
+        return
+    if a.summarize_counters:
+        print(summarize_counters(a.summarize_counters))
+        return
+    if a.traffic_from:
+        fetch_csv, write_csv = a.traffic_from.split(",")
+        print(json.dumps(traffic_from(fetch_csv, write_csv), indent=1))
+        return
     _lib.load()  # fail loudly without the HIP library
     dev = "cuda:0"
     torch.cuda.set_device(0)
