@@ -396,39 +396,6 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_fused(StrideAttentionParams p
   int32_t* btab = reinterpret_cast<int32_t*>(recs + p.max_pages * (RF + kHeadsPerGroup));
   const int nblk = min((last >> page_shift) + 1, (p.max_pages * kAttnPage + (1 << page_shift) - 1) >> page_shift);
   for (int i = t; i < nblk; i += 64 * NWV) btab[i] = p.kv.table[static_cast<int64_t>(slot) * p.kv.max_blocks + i];
-  // LIST: does the item list hold row j's pages where the engine's list puts them?
-  bool whole = true;
-  if constexpr (LIST) {
-    int s = 0;
-    for (int i = t; i < j; i += 64 * NWV) s += (p.row_pos[i] >> kAttnPageShift) + 1;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
-    if (lane == 0) part[wave] = s;
-    __syncthreads();
-    int off = 0;
-#pragma unroll
-    for (int w = 0; w < NWV; ++w) off += part[w];
-    int ok = off + pages <= p.item_count;
-    for (int c = t; ok && c < pages; c += 64 * NWV)
-      ok = p.items[2 * (off + c)] == j && p.items[2 * (off + c) + 1] == c;
-    whole = __syncthreads_and(ok) != 0;
-    if (!whole) {
-      for (int i = t; i < kListMaxPages / 32; i += 64 * NWV) listed[i] = 0u;
-      __syncthreads();
-      for (int i = t; i < p.item_count; i += 64 * NWV) {
-        const int c = p.items[2 * i + 1];
-        if (p.items[2 * i] == j && c >= 0 && c < pages) atomicOr(&listed[c >> 5], 1u << (c & 31));
-      }
-      __syncthreads();
-      // unlisted pages: the records an earlier call left in scratch
-      const float* src = p.scratch + static_cast<int64_t>(j * p.n_kv + g) * p.max_pages * p.rec_floats;
-      for (int u = t; u < pages * RF; u += 64 * NWV) {
-        const int c = u / RF, e = u % RF;
-        if (!((listed[c >> 5] >> (c & 31)) & 1u)) recs[c * RF + e] = src[static_cast<int64_t>(c) * p.rec_floats + e];
-      }
-    }
-  }
-  auto is_listed = [&](int page) { return !LIST || whole || ((listed[page >> 5] >> (page & 31)) & 1u); };
   const uint16_t* kv_base = static_cast<const uint16_t*>(p.kv.arena) + p.layer * p.kv.layer_elems + g * p.kv.group_elems;
   auto kv_at = [&](int which, int pos) {
     return kv_base + btab[pos >> page_shift] * p.kv.block_elems + which * p.kv.which_elems +
@@ -456,7 +423,20 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_fused(StrideAttentionParams p
 #pragma unroll
     for (int c = 0; c < kKey; ++c) kr[c] = load16(key + kEl * c);
   };
+  // LIST: does the item list hold row j's pages where the engine's list puts them?
+  // (The page counts of the rows before j are loaded before the first page, so
+  // the check's loads overlap that page's.)
+  int s = 0;
+  if constexpr (LIST)
+    for (int i = t; i < j; i += 64 * NWV) s += (p.row_pos[i] >> kAttnPageShift) + 1;
   if (wave < pages) fetch(wave);
+  // Round 0 runs before the list check completes and sums whichever pages it
+  // takes; if the check then fails, the unlisted pages' records are replaced
+  // from scratch before anything reads them.
+  bool whole = true, checked = !LIST;
+  int list_ok = 1, off_list = 0;
+  int32_t item_row = 0, item_page = 0;
+  auto is_listed = [&](int page) { return !checked || whole || ((listed[page >> 5] >> (page & 31)) & 1u); };
   for (int it = 0; it < rounds; ++it) {
     const int page = it * NWV + wave;
     const bool active = page < pages && is_listed(page);
@@ -469,7 +449,28 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_fused(StrideAttentionParams p
         *reinterpret_cast<u32x4*>(&vs[wave][P / (D / kEl)][(P % (D / kEl)) * kEl]) = vr[k];
       }
     }
+    if constexpr (LIST) {
+      if (it == 0) {
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
+        if (lane == 0) part[wave] = s;
+      }
+    }
     __syncthreads();  // this wave's V rows
+    if constexpr (LIST) {
+      if (it == 0) {  // row j's stretch of the list: loads issued now, compared at the end of the round
+#pragma unroll
+        for (int w = 0; w < NWV; ++w) off_list += part[w];
+        list_ok = off_list + pages <= p.item_count;
+        if (list_ok && t < pages) {
+          item_row = p.items[2 * (off_list + t)];
+          item_page = p.items[2 * (off_list + t) + 1];
+        } else {
+          item_row = j;
+          item_page = t;
+        }
+      }
+    }
     f32x4 mx = {0.f, 0.f, 0.f, 0.f};
     float sc[kHeadsPerGroup] = {0.f, 0.f, 0.f, 0.f};
     if (active) {
@@ -536,6 +537,32 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_fused(StrideAttentionParams p
       }
     }
     __syncthreads();  // the staging buffers are reused by the next round
+    if constexpr (LIST) {
+      if (it == 0) {
+        int ok = list_ok && item_row == j && item_page == t;
+        for (int c = t + 64 * NWV; ok && c < pages; c += 64 * NWV)  // rows of more pages than threads
+          ok = p.items[2 * (off_list + c)] == j && p.items[2 * (off_list + c) + 1] == c;
+        whole = __syncthreads_and(ok) != 0;
+        checked = true;
+        if (!whole) {
+          for (int i = t; i < kListMaxPages / 32; i += 64 * NWV) listed[i] = 0u;
+          __syncthreads();
+          for (int i = t; i < p.item_count; i += 64 * NWV) {
+            const int c = p.items[2 * i + 1];
+            if (p.items[2 * i] == j && c >= 0 && c < pages) atomicOr(&listed[c >> 5], 1u << (c & 31));
+          }
+          __syncthreads();
+          // unlisted pages: the records an earlier call left in scratch (over
+          // whatever round 0 summed for them)
+          const float* src = p.scratch + static_cast<int64_t>(j * p.n_kv + g) * p.max_pages * p.rec_floats;
+          for (int u = t; u < pages * RF; u += 64 * NWV) {
+            const int c = u / RF, e = u % RF;
+            if (!((listed[c >> 5] >> (c & 31)) & 1u)) recs[c * RF + e] = src[static_cast<int64_t>(c) * p.rec_floats + e];
+          }
+          __syncthreads();
+        }
+      }
+    }
   }
   if constexpr (LIST) {
     if (!whole) {  // store the summed records, as the page kernel does
