@@ -554,7 +554,10 @@ inline Pick pick_small(int T, int smax, int mats, int nseg, int per) {
       if (T <= 1) return {0, 55};
       if (T <= 2) return {0, 0};
       if (T <= 4) return {0, 5};
-      return {3, 30};  // plain weight loads (two lane groups share them through L2): 16.7 us at M = 128
+      // Non-temporal weight loads: in the measured decode step at M = 128 the step is
+      // 0.8-0.9 % faster than with plain loads (configuration 30, which the same op
+      // timed alone prefers by a few percent: 16.7 us).
+      return {3, 7};
     }
     return {0, T <= 2 ? 0 : (T <= 4 ? 5 : 33)};  // O: 5.1 / 5.0 / 5.7 / 7.1 us at M = 1 / 32 / 64 / 128
   }
