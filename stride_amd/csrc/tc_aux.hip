@@ -211,6 +211,9 @@ __global__ __launch_bounds__(64) void k_attn_page(StrideAttentionParams p, int p
   const int lane = threadIdx.x;
   const int j = p.items[2 * item];
   const int page = p.items[2 * item + 1];
+  // An item outside the record array (page >= max_pages) would write into the next
+  // row's records: it is skipped (the caller sizes max_pages for its longest row).
+  if (page < 0 || page >= p.max_pages) return;
   const int slot = p.row_slot[j];
   const int visible = p.row_pos[j] + 1;
   const int p0 = page << kAttnPageShift;
@@ -317,7 +320,7 @@ __global__ __launch_bounds__(256) void k_attn_combine(StrideAttentionParams p) {
   const int j = blockIdx.x / p.n_kv;
   const int g = blockIdx.x % p.n_kv;
   const int t = threadIdx.x;
-  const int pages = (p.row_pos[j] >> kAttnPageShift) + 1;
+  const int pages = min((p.row_pos[j] >> kAttnPageShift) + 1, p.max_pages);  // row_pos < 64 * max_pages
   const int rf = p.rec_floats;
   const float* src = p.scratch + static_cast<int64_t>(j * p.n_kv + g) * p.max_pages * rf;
   for (int i = t; i < pages * rf; i += 256) recs[i] = src[i];
