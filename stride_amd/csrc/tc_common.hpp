@@ -93,7 +93,8 @@ __device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
 // +7), B 16 k x 32 lanes (lane l: lane l%32, same k), C 32 x 32 (lane l: lane
 // l%32, rows 8*(i/4) + 4*(l/32) + i%4). Two of them over k 0-15 then 16-31 give
 // the same bits as one v_mfma_f32_16x16x32_bf16 per 16x16 tile over the 32-column
-// chunk (checked on the device by the shape-equivalence probe).
+// chunk (checked on the device by the shape-equivalence known-answer test,
+// tests/test_gpu_kat.py).
 __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
 }
