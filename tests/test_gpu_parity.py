@@ -100,7 +100,7 @@ def test_config1_bf16_rounding_alone_fails_the_bound(exact):
                                    # the Llama-3.2-1B O and down shapes at the benchmark's M = 128
                                    (128, 2048, 2048), (128, 2048, 8192),
                                    # the same shapes in the prefill regime (LDS-pipelined kernels)
-                                   (1024, 2048, 2048), (2048, 2048, 8192)])
+                                   (1024, 2048, 2048), (2048, 2048, 8192), (4096, 2048, 2048)])
 def test_gemm_residual(exact, m, n, k):
     w, xb, x = make(1, m, n, k)
     h = synth.f32_normal(1, Ids.H, m, n)
@@ -139,7 +139,7 @@ def test_lm_full(exact, m, n, k):
 # and 256 x 256 pipeline configurations.
 @pytest.mark.parametrize("m,n,k", [(1, 256, 2048), (9, 128, 2048), (128, 64, 2048), (150, 64, 512), (9, 128, 2064),
                                    (5, 8192, 2048), (64, 8192, 2048), (128, 8192, 2048), (140, 8192, 2048),
-                                   (290, 8192, 2048), (1024, 8192, 2048)])
+                                   (290, 8192, 2048), (1024, 8192, 2048), (2048, 8192, 2048)])
 def test_mlp13(exact, m, n, k):
     w1 = synth.bf16_normal(3, Ids.W1, n, k, 0.02)
     w3 = synth.bf16_normal(3, Ids.W3, n, k, 0.02)
