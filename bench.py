@@ -58,6 +58,9 @@ def parse():
     ap.add_argument("--step-only", type=int, default=0,
                     help="run only the measured steps (host-launched, no graph, no per-op timing; for kernel "
                     "profiles of the step as it is measured) and print its time")
+    ap.add_argument("--exact-step", type=int, default=0,
+                    help="time the exact FP32 path's whole decode step (random-init Llama-3.2-1B, fp32 weights, "
+                    "batch 1 and 32, position 100) and print its JSON")
     ap.add_argument("--summarize-trace", default="",
                     help="print per-kernel launch counts and durations from a rocprofv3 kernel_trace.csv and exit")
     ap.add_argument("--summarize-counters", default="",
@@ -516,6 +519,33 @@ def engine_step(torch, dev, m, steps, warmup, position=383):
                    "tc_gemm_residual), tc_norm, tc_lm_greedy"}
 
 
+def exact_step(torch, batches=(1, 32), steps=5):
+    """The exact FP32 path end to end on the GPU (stride_amd.exact_engine over the
+    stride_k_* kernels, bit-identical to the reference's CPU exact path): one greedy
+    decode step of random-init Llama-3.2-1B with fp32 weights (4.9 GB read per step),
+    host-launched, every row at position 100."""
+    from stride_amd import exact_engine as E
+    from stride_amd.weights import ModelConfig
+
+    cfg = ModelConfig()
+    model = E.ExactModel.random(cfg, seed=7, max_positions=512)
+    be = E.GpuBackend("cuda:0")
+    out = {}
+    for m in batches:
+        eng = E.ExactEngine(model, be, slots=m, max_ctx=512, max_rows=m)
+        rows = [(j, 100, 7 + j) for j in range(m)]
+        eng.step(rows, greedy=list(range(m)))
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            eng.step(rows, greedy=list(range(m)))
+        torch.cuda.synchronize()
+        dt = (time.perf_counter() - t0) / steps
+        out[str(m)] = {"ms_per_step": round(dt * 1e3, 3), "tok_s": round(m / dt, 1)}
+        del eng
+    return out
+
+
 def library_gemm(torch, dev, ms=(128, 2048, 4096)):
     """Context for both rooflines: the vendor library (torch.matmul, which calls
     hipBLASLt) on the same shapes in bf16 (gate+up as one 16384-row matmul, no
@@ -573,6 +603,9 @@ def main():
     _lib.load()  # fail loudly without the HIP library
     dev = "cuda:0"
     torch.cuda.set_device(0)
+    if a.exact_step:
+        print(json.dumps({"exact_decode_step": exact_step(torch)}), flush=True)
+        return
     if a.engine_only:
         print(json.dumps({"full_decode_step": engine_step(torch, dev, a.m, a.steps, a.warmup)}), flush=True)
         return
