@@ -52,6 +52,21 @@ __device__ __forceinline__ Segment seg_at(const Geometry& g, int i) {
   return i == 0 ? g.seg[0] : (i == 1 ? g.seg[1] : g.seg[2]);
 }
 
+// Row tile rt of the segments laid end to end: its segment, and its index there.
+__device__ __forceinline__ int flat_segment(const Geometry& g, int rt, int& local) {
+  const int r0 = g.seg[0].row_tiles, r1 = g.seg[1].row_tiles;
+  if (rt < r0) {
+    local = rt;
+    return 0;
+  }
+  if (rt < r0 + r1) {
+    local = rt - r0;
+    return 1;
+  }
+  local = rt - r0 - r1;
+  return 2;
+}
+
 // Segment of logical row block rb (made segment-relative), with `per` logical
 // blocks per row block of a segment's count.
 __device__ __forceinline__ int locate_segment(const Geometry& g, int& rb, int per = 1) {

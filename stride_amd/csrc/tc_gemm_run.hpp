@@ -76,78 +76,83 @@ inline bool mat_ok(const StrideGemmMat& m, const char* name, std::string& why) {
 
 // Decode-regime configurations of k_stream: (R row tiles per wave, LT lane tiles,
 // WS split waves, WR row waves, U chunks per batch, XL x staged in LDS, XS one
-// split per workgroup, the last arriving workgroup of a tile group combining). Which
+// split per workgroup, the last arriving workgroup of a tile group combining, F
+// flat row blocks over all segments, which may straddle the fused QKV's Q/K/V
+// boundaries: each row tile reads its own segment's weights and goes to its own
+// segment's epilogue). Which
 // one runs never changes results: all evaluate the same chunk order and the same
 // split combine. The table is indexed by stride_tc_set_stream_config() for tuning
 // sweeps and by pick_decode() otherwise.
 #define STRIDE_TC_DECODE_CONFIGS(S) \
-  S(0, 1, 1, 8, 1, 8, false, false) \
-  S(1, 1, 1, 8, 1, 4, false, false) \
-  S(2, 1, 1, 2, 4, 8, false, false) \
-  S(3, 1, 1, 1, 8, 8, false, false) \
-  S(4, 1, 1, 1, 4, 8, false, false) \
-  S(5, 1, 2, 8, 1, 8, false, false) \
-  S(6, 1, 2, 2, 4, 8, false, false) \
-  S(7, 1, 2, 1, 8, 8, false, false) \
-  S(8, 1, 4, 8, 1, 4, false, false) \
-  S(9, 2, 4, 8, 1, 2, false, false) \
-  S(10, 1, 4, 2, 4, 4, false, false) \
-  S(11, 1, 4, 2, 4, 2, true, false) \
-  S(12, 1, 4, 1, 8, 4, false, false) \
-  S(13, 2, 4, 1, 8, 2, true, false) \
-  S(14, 1, 8, 8, 1, 2, false, false) \
-  S(15, 2, 8, 8, 1, 2, false, false) \
-  S(16, 1, 8, 1, 8, 2, true, false) \
-  S(17, 1, 8, 1, 8, 2, false, false) \
-  S(18, 1, 1, 16, 1, 4, false, false) \
-  S(19, 1, 1, 16, 1, 8, false, false) \
-  S(20, 1, 2, 16, 1, 4, false, false) \
-  S(21, 1, 4, 16, 1, 2, false, false) \
-  S(22, 1, 2, 4, 2, 4, false, false) \
-  S(23, 1, 1, 4, 2, 8, false, false) \
-  S(24, 1, 4, 4, 2, 4, false, false) \
-  S(25, 1, 2, 16, 1, 2, false, false) \
-  S(26, 1, 1, 16, 1, 2, false, false) \
-  S(27, 2, 4, 8, 1, 4, false, false) \
-  S(28, 2, 8, 8, 1, 1, false, false) \
-  S(29, 4, 4, 8, 1, 1, false, false) \
-  S(30, 4, 8, 8, 1, 1, false, false) \
-  S(31, 2, 8, 8, 2, 1, true, false) \
-  S(32, 1, 8, 8, 2, 1, true, false) \
-  S(33, 2, 2, 8, 1, 4, false, false) \
-  S(34, 1, 1, 8, 2, 8, false, false) \
-  S(35, 2, 1, 8, 1, 8, false, false) \
-  S(36, 1, 4, 2, 4, 8, true, false) \
-  S(37, 1, 8, 2, 4, 8, true, false) \
-  S(38, 2, 4, 2, 4, 8, true, false) \
-  S(39, 1, 8, 1, 8, 4, true, false) \
-  S(40, 2, 8, 1, 8, 4, true, false) \
-  S(41, 1, 4, 2, 8, 8, true, false) \
-  S(42, 2, 8, 2, 4, 4, true, false) \
-  S(43, 1, 8, 1, 4, 8, true, true) \
-  S(44, 2, 8, 1, 4, 4, true, true) \
-  S(45, 1, 8, 1, 8, 8, true, true) \
-  S(46, 1, 8, 1, 2, 4, true, true) \
-  S(47, 1, 4, 1, 4, 8, true, true) \
-  S(48, 2, 4, 1, 4, 4, true, true) \
-  S(49, 1, 8, 1, 4, 4, true, true) \
-  S(50, 2, 8, 1, 2, 4, true, true) \
-  S(51, 4, 8, 1, 2, 2, true, true) \
-  S(52, 2, 8, 1, 4, 2, true, true) \
-  S(53, 1, 1, 1, 4, 8, false, true) \
-  S(54, 1, 1, 1, 8, 8, false, true) \
-  S(55, 1, 1, 1, 2, 8, false, true) \
-  S(56, 2, 1, 1, 4, 4, false, true) \
-  S(57, 1, 2, 1, 4, 8, false, true) \
-  S(58, 1, 8, 1, 4, 8, false, true) \
-  S(59, 2, 2, 4, 1, 4, false, false)
+  S(0, 1, 1, 8, 1, 8, false, false, false) \
+  S(1, 1, 1, 8, 1, 4, false, false, false) \
+  S(2, 1, 1, 2, 4, 8, false, false, false) \
+  S(3, 1, 1, 1, 8, 8, false, false, false) \
+  S(4, 1, 1, 1, 4, 8, false, false, false) \
+  S(5, 1, 2, 8, 1, 8, false, false, false) \
+  S(6, 1, 2, 2, 4, 8, false, false, false) \
+  S(7, 1, 2, 1, 8, 8, false, false, false) \
+  S(8, 1, 4, 8, 1, 4, false, false, false) \
+  S(9, 2, 4, 8, 1, 2, false, false, false) \
+  S(10, 1, 4, 2, 4, 4, false, false, false) \
+  S(11, 1, 4, 2, 4, 2, true, false, false) \
+  S(12, 1, 4, 1, 8, 4, false, false, false) \
+  S(13, 2, 4, 1, 8, 2, true, false, false) \
+  S(14, 1, 8, 8, 1, 2, false, false, false) \
+  S(15, 2, 8, 8, 1, 2, false, false, false) \
+  S(16, 1, 8, 1, 8, 2, true, false, false) \
+  S(17, 1, 8, 1, 8, 2, false, false, false) \
+  S(18, 1, 1, 16, 1, 4, false, false, false) \
+  S(19, 1, 1, 16, 1, 8, false, false, false) \
+  S(20, 1, 2, 16, 1, 4, false, false, false) \
+  S(21, 1, 4, 16, 1, 2, false, false, false) \
+  S(22, 1, 2, 4, 2, 4, false, false, false) \
+  S(23, 1, 1, 4, 2, 8, false, false, false) \
+  S(24, 1, 4, 4, 2, 4, false, false, false) \
+  S(25, 1, 2, 16, 1, 2, false, false, false) \
+  S(26, 1, 1, 16, 1, 2, false, false, false) \
+  S(27, 2, 4, 8, 1, 4, false, false, false) \
+  S(28, 2, 8, 8, 1, 1, false, false, false) \
+  S(29, 4, 4, 8, 1, 1, false, false, false) \
+  S(30, 4, 8, 8, 1, 1, false, false, false) \
+  S(31, 2, 8, 8, 2, 1, true, false, false) \
+  S(32, 1, 8, 8, 2, 1, true, false, false) \
+  S(33, 2, 2, 8, 1, 4, false, false, false) \
+  S(34, 1, 1, 8, 2, 8, false, false, false) \
+  S(35, 2, 1, 8, 1, 8, false, false, false) \
+  S(36, 1, 4, 2, 4, 8, true, false, false) \
+  S(37, 1, 8, 2, 4, 8, true, false, false) \
+  S(38, 2, 4, 2, 4, 8, true, false, false) \
+  S(39, 1, 8, 1, 8, 4, true, false, false) \
+  S(40, 2, 8, 1, 8, 4, true, false, false) \
+  S(41, 1, 4, 2, 8, 8, true, false, false) \
+  S(42, 2, 8, 2, 4, 4, true, false, false) \
+  S(43, 1, 8, 1, 4, 8, true, true, false) \
+  S(44, 2, 8, 1, 4, 4, true, true, false) \
+  S(45, 1, 8, 1, 8, 8, true, true, false) \
+  S(46, 1, 8, 1, 2, 4, true, true, false) \
+  S(47, 1, 4, 1, 4, 8, true, true, false) \
+  S(48, 2, 4, 1, 4, 4, true, true, false) \
+  S(49, 1, 8, 1, 4, 4, true, true, false) \
+  S(50, 2, 8, 1, 2, 4, true, true, false) \
+  S(51, 4, 8, 1, 2, 2, true, true, false) \
+  S(52, 2, 8, 1, 4, 2, true, true, false) \
+  S(53, 1, 1, 1, 4, 8, false, true, false) \
+  S(54, 1, 1, 1, 8, 8, false, true, false) \
+  S(55, 1, 1, 1, 2, 8, false, true, false) \
+  S(56, 2, 1, 1, 4, 4, false, true, false) \
+  S(57, 1, 2, 1, 4, 8, false, true, false) \
+  S(58, 1, 8, 1, 4, 8, false, true, false) \
+  S(59, 2, 2, 4, 1, 4, false, false, false) \
+  S(60, 3, 2, 8, 1, 4, false, false, true) \
+  S(61, 3, 2, 4, 1, 8, false, false, true)
 
 struct DecodeCfg {
   int r, lt, ws, wr, u;
-  bool xl, xs;
+  bool xl, xs, flat;
 };
 
-#define STRIDE_TC_ROW(i, R, LT, WS, WR, U, XL, XS) {R, LT, WS, WR, U, XL, XS},
+#define STRIDE_TC_ROW(i, R, LT, WS, WR, U, XL, XS, F) {R, LT, WS, WR, U, XL, XS, F},
 constexpr DecodeCfg kDecodeCfgs[] = {STRIDE_TC_DECODE_CONFIGS(STRIDE_TC_ROW)};
 #undef STRIDE_TC_ROW
 constexpr int kNumDecodeCfgs = sizeof(kDecodeCfgs) / sizeof(kDecodeCfgs[0]);
@@ -172,27 +177,35 @@ struct ScratchSet {
 ScratchSet scratch_for(hipStream_t st);
 extern int g_last_cfg;  // configuration of the last decode-regime launch (-2: prefill kernel)
 
-template <class Epi, int R, int LT, int WS, int WR, int U, bool XL, bool XS>
+template <class Epi, int R, int LT, int WS, int WR, int U, bool XL, bool XS, bool F>
 void launch_stream(Geometry g, const typename Epi::Out& o, hipStream_t st) {
-  if constexpr (XS && Epi::kReduce) {
+  if constexpr ((XS && Epi::kReduce) || (F && (XS || Epi::kReduce || Epi::kInitFromOutput))) {
     return;  // never selected (decode_cfg_fits)
   } else {
     int blocks = 0;
-    for (int i = 0; i < g.nseg; ++i) {
-      g.seg[i].blocks = (g.seg[i].row_tiles + WR * R - 1) / (WR * R);
-      blocks += XS ? g.seg[i].blocks * g.seg[i].splits : g.seg[i].blocks;
+    if constexpr (F) {  // one range of row tiles over all segments
+      int total = 0;
+      for (int i = 0; i < g.nseg; ++i) total += g.seg[i].row_tiles;
+      for (int i = g.nseg; i < 3; ++i) g.seg[i].row_tiles = 0;
+      for (int i = 1; i < 3; ++i) g.seg[i].blocks = 0;
+      g.seg[0].blocks = blocks = (total + WR * R - 1) / (WR * R);
+    } else {
+      for (int i = 0; i < g.nseg; ++i) {
+        g.seg[i].blocks = (g.seg[i].row_tiles + WR * R - 1) / (WR * R);
+        blocks += XS ? g.seg[i].blocks * g.seg[i].splits : g.seg[i].blocks;
+      }
     }
     blocks *= (g.lane_groups + LT - 1) / LT;
-    hipLaunchKernelGGL((k_stream<Epi, R, LT, WS, WR, U, XL, XS>), dim3(blocks), dim3(kWave * WS * WR), 0, st, g, o);
+    hipLaunchKernelGGL((k_stream<Epi, R, LT, WS, WR, U, XL, XS, F>), dim3(blocks), dim3(kWave * WS * WR), 0, st, g, o);
   }
 }
 
 template <class Epi>
 void launch_decode_cfg(int idx, const Geometry& g, const typename Epi::Out& o, hipStream_t st) {
   switch (idx) {
-#define STRIDE_TC_CASE(i, R, LT, WS, WR, U, XL, XS)          \
-  case i:                                                    \
-    launch_stream<Epi, R, LT, WS, WR, U, XL, XS>(g, o, st); \
+#define STRIDE_TC_CASE(i, R, LT, WS, WR, U, XL, XS, F)          \
+  case i:                                                       \
+    launch_stream<Epi, R, LT, WS, WR, U, XL, XS, F>(g, o, st); \
     break;
     STRIDE_TC_DECODE_CONFIGS(STRIDE_TC_CASE)
 #undef STRIDE_TC_CASE
@@ -217,6 +230,11 @@ inline bool decode_cfg_fits(const DecodeCfg& c, Geometry g, int smax, int mats, 
     u = u < umax ? u : umax;  // as k_stream clamps it
   }
   const int chunks = g.col_tiles >> 1;
+  if (c.flat) {
+    if (c.xs || reduce || g.nseg < 2) return false;
+    for (int i = 1; i < g.nseg; ++i)
+      if (g.seg[i].splits != g.seg[0].splits) return false;
+  }
   if (c.xs) {
     if (reduce || c.ws != 1 || smax < 2 || smax > kMaxXSplits) return false;
     if (total_tiles(g) * smax * mats * 1024 > kScratchBytes) return false;
@@ -552,14 +570,18 @@ inline Pick pick_small(int T, int smax, int mats, int nseg, int per) {
     return {3, 31};
   }
   if (smax == 4) {  // the split rule's few-row matrices; per = chunks per split (down: 64, O and QKV: 16)
-    if (nseg == 3) return {0, T <= 1 ? 0 : (T <= 2 ? 5 : (T <= 4 ? 33 : 27))};  // QKV: 6.3 / 7.0 / 8.3 / 10.0 us at M = 1 / 32 / 64 / 128
-    if (per >= 32) {  // down: 11.2 / 11.9 / 14.5 / 16.7 us at M = 1 / 32 / 64 / 128
+    // QKV: 6.3 / 7.0 / 8.3 / 9.3 us at M = 1 / 32 / 64 / 128. From five lane tiles the
+    // flat row blocks of three row tiles (straddling the Q/K/V boundaries) fill all
+    // 256 CUs with 64 x 4 workgroups (9.3 against 9.7 us for 2-tile blocks at M = 128).
+    if (nseg == 3) return {0, T <= 1 ? 0 : (T <= 2 ? 5 : (T <= 4 ? 33 : 60))};
+    if (per >= 32) {  // down: 11.2 / 11.9 / 14.5 / 15.9 us at M = 1 / 32 / 64 / 128
       if (T <= 1) return {0, 55};
-      if (T <= 2) return {0, 0};
-      if (T <= 4) return {0, 5};
+      // Two lane tiles, two waves, one split per workgroup: 1.5-3 % faster decode
+      // steps at M = 32-64 than the streaming kernel (configurations 0 and 5).
+      if (T <= 4) return {3, 15};
       // Non-temporal weight loads: in the measured decode step at M = 128 the step is
-      // 0.8-0.9 % faster than with plain loads (configuration 30, which the same op
-      // timed alone prefers by a few percent: 16.7 us).
+      // 0.9 % faster than with plain loads (configuration 30, which the same op
+      // timed alone prefers: 14.9 against 15.7 us).
       return {3, 7};
     }
     return {0, T <= 2 ? 0 : (T <= 4 ? 5 : 33)};  // O: 5.1 / 5.0 / 5.7 / 7.1 us at M = 1 / 32 / 64 / 128

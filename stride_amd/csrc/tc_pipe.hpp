@@ -38,21 +38,6 @@ constexpr int vm_lgkm0_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 <
 // lgkmcnt = 0 only (vmcnt and expcnt at their no-wait maxima).
 constexpr int lgkm0_imm() { return vmcnt_imm(63) & ~(0xF << 8); }
 
-// Row tile rt of the segments laid end to end: its segment, and its index there.
-__device__ __forceinline__ int flat_segment(const Geometry& g, int rt, int& local) {
-  const int r0 = g.seg[0].row_tiles, r1 = g.seg[1].row_tiles;
-  if (rt < r0) {
-    local = rt;
-    return 0;
-  }
-  if (rt < r0 + r1) {
-    local = rt - r0;
-    return 1;
-  }
-  local = rt - r0 - r1;
-  return 2;
-}
-
 // FLAT: the segments' row tiles form one range (they share the split count), so
 // a block may straddle two segments; each row tile reads its own segment's
 // weights and goes to its own segment's epilogue. This lets the block height be

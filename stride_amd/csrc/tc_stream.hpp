@@ -27,6 +27,9 @@ constexpr int kMaxXSplits = 8;
 // word 3 of a raw, untyped buffer resource.
 constexpr int kCachePolicySc1 = 16;
 constexpr int kRawBufferWord3 = 0x00020000;
+// s_waitcnt immediate for vmcnt(0) with expcnt and lgkmcnt left at their
+// no-wait maxima.
+constexpr int kVmcnt0 = 0x0F70;
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 
 // Output-tile and unit bases of segment si for the cross-workgroup split scratch.
@@ -52,6 +55,64 @@ __device__ __forceinline__ int xs_unit0(const Geometry& g, int si) {
 // ascending order, y = ((c0 + c1) + c2) + ..., applies the epilogue and re-arms
 // the counter for the next launch. Nothing waits on another workgroup. Rows
 // rt_first .. rt_first+R-1 and lane tiles lt0 .. lt0+nlt-1 are this wave's.
+// Fold of the last arriving workgroup of a cross-workgroup split unit, for a
+// split count S known at compile time. Every split's partial tile is loaded back
+// (its own too: it was stored before the arrival count, and the copy is
+// bit-identical), in batches of up to 16 loads across tiles, so a batch costs
+// one memory round trip rather than one per tile; each tile is then folded in
+// ascending split order, and the batch's epilogue stores go out together.
+template <class Epi, int R, int LT, int S, class Off>
+__device__ __forceinline__ void xs_fold(const Geometry& g, const typename Epi::Out& o, int si, const Segment& sg,
+                                        int rt_first, int lt0, int nlt, int lane, __amdgpu_buffer_rsrc_t part,
+                                        Off offset) {
+  constexpr int M = Epi::kMats;
+  constexpr int T = R * LT;
+  constexpr int TB0 = 16 / (S * M);
+  constexpr int TB = TB0 < 1 ? 1 : (TB0 > T ? T : TB0);  // tiles per batch
+  unroll<(T + TB - 1) / TB>([&](auto batch) {
+    constexpr int t0 = decltype(batch)::value * TB;
+    f32x4 pv[TB][S][M];
+    unroll<TB>([&](auto i) {
+      constexpr int t = t0 + decltype(i)::value;
+      if constexpr (t < T) {
+        // Tiles past the matrix or the live lanes have no partials (their
+        // offsets could lie past the scratch): they load the last live tile's
+        // instead, and their sums are discarded. Unconditional loads stay
+        // together ahead of the folds.
+        const int r = min(rt_first + t / LT, sg.row_tiles - 1) - rt_first;
+        const int l = min(t % LT, nlt - 1);
+#pragma unroll
+        for (int s = 0; s < S; ++s)
+#pragma unroll
+          for (int m = 0; m < M; ++m)
+            pv[decltype(i)::value][s][m] = __builtin_bit_cast(
+                f32x4, __builtin_amdgcn_raw_buffer_load_b128(part, offset(r, l, s, m), 0, kCachePolicySc1));
+      }
+    });
+    // All of the batch's loads have landed before the first fold; without this
+    // wait the compiler, which cannot tell that the tile conditions are
+    // wave-uniform, waits per tile with vmcnt(0) after the previous tile's
+    // epilogue store, paying each store's round trip.
+    __builtin_amdgcn_s_waitcnt(kVmcnt0);
+    f32x4 y[TB][M];
+    unroll<TB>([&](auto i) {
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        y[decltype(i)::value][m] = pv[decltype(i)::value][0][m];
+#pragma unroll
+        for (int s = 1; s < S; ++s) y[decltype(i)::value][m] = y[decltype(i)::value][m] + pv[decltype(i)::value][s][m];
+      }
+    });
+    unroll<TB>([&](auto i) {
+      constexpr int t = t0 + decltype(i)::value;
+      if constexpr (t < T) {
+        constexpr int r = t / LT, l = t % LT;
+        if (rt_first + r < sg.row_tiles && l < nlt) Epi::apply(o, g, si, rt_first + r, lt0 + l, y[decltype(i)::value], lane);
+      }
+    });
+  });
+}
+
 template <class Epi, int R, int LT>
 __device__ __forceinline__ void xs_finish(const Geometry& g, const typename Epi::Out& o, int si, const Segment& sg,
                                           int rt_first, int lt0, int nlt, int* cnt, int splits, int my_split,
@@ -115,40 +176,45 @@ __device__ __forceinline__ void xs_finish(const Geometry& g, const typename Epi:
   // partial loads below stay after the barrier that published `last`.
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
   if (!last) return;
+  if (splits == 4) {
+    xs_fold<Epi, R, LT, 4>(g, o, si, sg, rt_first, lt0, nlt, lane, part, offset);
+  } else if (splits == 8) {
+    xs_fold<Epi, R, LT, 8>(g, o, si, sg, rt_first, lt0, nlt, lane, part, offset);
+  } else {
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    if (rt_first + r >= sg.row_tiles) continue;
+    for (int r = 0; r < R; ++r) {
+      if (rt_first + r >= sg.row_tiles) continue;
 #pragma unroll
-    for (int l = 0; l < LT; ++l) {
-      if (l >= nlt) continue;
-      // Issue every partial load first (at most kMaxXSplits splits, a
-      // wave-uniform bound), then fold in ascending split order.
-      f32x4 pv[kMaxXSplits][M];
+      for (int l = 0; l < LT; ++l) {
+        if (l >= nlt) continue;
+        f32x4 pv[kMaxXSplits][M];
 #pragma unroll
-      for (int s = 0; s < kMaxXSplits; ++s) {
-        if (s >= splits || s == my_split) continue;
+        for (int s = 0; s < kMaxXSplits; ++s) {
+          if (s >= splits || s == my_split) continue;
 #pragma unroll
-        for (int m = 0; m < M; ++m)
-          pv[s][m] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(part, offset(r, l, s, m), 0, kCachePolicySc1));
-      }
-      f32x4 y[M];
-#pragma unroll
-      for (int s = 0; s < kMaxXSplits; ++s) {
-        if (s >= splits) continue;
-#pragma unroll
-        for (int m = 0; m < M; ++m) {
-          const f32x4 v = s == my_split ? acc[m][r][l] : pv[s][m];
-          y[m] = s == 0 ? v : y[m] + v;
+          for (int m = 0; m < M; ++m)
+            pv[s][m] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(part, offset(r, l, s, m), 0, kCachePolicySc1));
         }
+        f32x4 y[M];
+#pragma unroll
+        for (int s = 0; s < kMaxXSplits; ++s) {
+          if (s >= splits) continue;
+#pragma unroll
+          for (int m = 0; m < M; ++m) {
+            const f32x4 v = s == my_split ? acc[m][r][l] : pv[s][m];
+            y[m] = s == 0 ? v : y[m] + v;
+          }
+        }
+        Epi::apply(o, g, si, rt_first + r, lt0 + l, y, lane);
       }
-      Epi::apply(o, g, si, rt_first + r, lt0 + l, y, lane);
     }
   }
 }
 
-template <class Epi, int R, int LT, int WS, int WR, int UC, bool XLC, bool XS>
+template <class Epi, int R, int LT, int WS, int WR, int UC, bool XLC, bool XS, bool FLAT = false>
 __global__ __launch_bounds__(kWave * WS * WR) void k_stream(Geometry g, typename Epi::Out o) {
   static_assert(!XS || (WS == 1 && !Epi::kReduce), "cross-workgroup splits use one split group and a plain epilogue");
+  static_assert(!FLAT || (!XS && !Epi::kReduce && !Epi::kInitFromOutput), "flat row blocks serve plain split-group launches");
   constexpr int M = Epi::kMats;
   // UC counts weight chunks in flight per batch; a paired GEMM loads M chunks per step.
   constexpr int U0 = UC / M > 0 ? UC / M : 1;
@@ -195,10 +261,14 @@ __global__ __launch_bounds__(kWave * WS * WR) void k_stream(Geometry g, typename
     const int bps = seg_at(g, si).blocks;
     xsplit = rb / bps;
     rb -= xsplit * bps;
-  } else {
+  } else if constexpr (!FLAT) {
     si = locate_segment(g, rb);
   }
   const Segment sg = seg_at(g, si);
+  // Row tiles of this block's range (FLAT: the segments laid end to end, which
+  // share the split count; the host sets seg[0].blocks to the whole range's row
+  // blocks, so a block may straddle two segments).
+  const int total = FLAT ? g.seg[0].row_tiles + g.seg[1].row_tiles + g.seg[2].row_tiles : sg.row_tiles;
   const int rt_first = rb * (WR * R) + wr * R;
   const int nlt = min(LT, g.lane_groups - lt0);
   const int chunks = g.col_tiles >> 1;
@@ -214,8 +284,14 @@ __global__ __launch_bounds__(kWave * WS * WR) void k_stream(Geometry g, typename
   for (int m = 0; m < M; ++m)
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const int rt = min(rt_first + r, sg.row_tiles - 1);
-      wp[m][r] = reinterpret_cast<const char*>(sg.w[m] + rt * strip) + off;
+      const int rt = min(rt_first + r, total - 1);
+      if constexpr (FLAT) {
+        int local = 0;
+        const Segment ss = seg_at(g, flat_segment(g, rt, local));
+        wp[m][r] = reinterpret_cast<const char*>((m == 0 ? ss.w[0] : ss.w[1]) + local * strip) + off;
+      } else {
+        wp[m][r] = reinterpret_cast<const char*>(sg.w[m] + rt * strip) + off;
+      }
     }
   const char* xp[LT];
 #pragma unroll
@@ -451,14 +527,16 @@ __global__ __launch_bounds__(kWave * WS * WR) void k_stream(Geometry g, typename
   } else if constexpr (WS == 1) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      if (rt_first + r >= sg.row_tiles) continue;
+      if (rt_first + r >= total) continue;
+      int rt = rt_first + r, ts = si;
+      if constexpr (FLAT) ts = flat_segment(g, rt_first + r, rt);
 #pragma unroll
       for (int l = 0; l < LT; ++l) {
         if (l >= nlt) continue;
         f32x4 y[M];
 #pragma unroll
         for (int m = 0; m < M; ++m) y[m] = acc[m][r][l];
-        Epi::apply(o, g, si, rt_first + r, lt0 + l, y, lane);
+        Epi::apply(o, g, ts, rt, lt0 + l, y, lane);
       }
     }
   } else {
@@ -479,12 +557,13 @@ __global__ __launch_bounds__(kWave * WS * WR) void k_stream(Geometry g, typename
     }
     for (int t = wave; t < WR * R * LT; t += WS * WR) {
       const int twr = t / (R * LT), r = (t / LT) % R, l = t % LT;
-      const int rt = rb * (WR * R) + twr * R + r;
-      if (l >= nlt || rt >= sg.row_tiles) continue;
+      int rt = rb * (WR * R) + twr * R + r, ts = si;
+      if (l >= nlt || rt >= total) continue;
+      if constexpr (FLAT) ts = flat_segment(g, rb * (WR * R) + twr * R + r, rt);
       f32x4 y[M];
 #pragma unroll
       for (int m = 0; m < M; ++m) y[m] = ybuf[(((twr * M + m) * R + r) * LT + l) * kWave + lane];
-      Epi::apply(o, g, si, rt, lt0 + l, y, lane);
+      Epi::apply(o, g, ts, rt, lt0 + l, y, lane);
     }
   }
 }
