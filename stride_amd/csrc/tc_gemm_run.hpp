@@ -476,7 +476,9 @@ void launch_pipe(Geometry g, const typename Epi::Out& o, int smax, hipStream_t s
   X(38, 4, 2, 2, 4, 1, 4, 2, 0) \
   X(39, 2, 2, 4, 4, 2, 3, 1, 0)
 
-constexpr int kNumPipeCfgs = 40;
+#define STRIDE_TC_PIPE_ONE(i, WRT, WLT, WM, WN, KC, NS, OCC, MF) +1
+constexpr int kNumPipeCfgs = 0 STRIDE_TC_PIPE_CONFIGS(STRIDE_TC_PIPE_ONE);
+#undef STRIDE_TC_PIPE_ONE
 extern int g_forced_pipe;
 
 template <class Epi>
