@@ -29,7 +29,7 @@ def setup():
     def w(n, k, rows=None):
         return layout.pack_tiles((torch.randn(n, k, generator=g, device=DEV) * 0.02).to(torch.bfloat16).view(torch.int16), rows)
 
-    W = dict(o=w(2048, 2048), down=w(512, 8192), w1=w(1024, 2048), w3=w(1024, 2048), w1b=w(8192, 2048), w3b=w(8192, 2048), lm=w(4000, 2048), lm1=w(16400, 2048),
+    W = dict(o=w(2048, 2048), o_odd=w(592, 2048), down=w(512, 8192), w1=w(1024, 2048), w3=w(1024, 2048), w1b=w(8192, 2048), w3b=w(8192, 2048), lm=w(4000, 2048), lm1=w(16400, 2048),
              q=w(512, 2048, layout.rope_rows(512, 64)), k=w(128, 2048, layout.rope_rows(128, 64)),
              v=w(128, 2048, layout.rope_rows(128, 64)))
     x = {k: (torch.randn(128, k, generator=g, device=DEV)).to(torch.bfloat16).view(torch.int16) for k in (2048, 8192)}
@@ -44,6 +44,11 @@ def run_all(W, x, h, m):
     ht = layout.lane_tiles(h[:m].clone())
     harness.gemm_residual(W["o"], xt, ht, m)
     out["o"] = digest(ht)
+    # 37 row tiles: every row blocking leaves a partial last block, whose missing
+    # tiles the cross-workgroup split fold must skip
+    ho = layout.lane_tiles(h[:m, :592].clone())
+    harness.gemm_residual(W["o_odd"], xt, ho, m)
+    out["o_odd"] = digest(ho)
     hd = layout.lane_tiles(h[:m, :512].clone())
     harness.gemm_residual(W["down"], layout.lane_tiles(x[8192][:m]), hd, m)
     out["down"] = digest(hd)
