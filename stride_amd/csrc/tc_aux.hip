@@ -372,14 +372,6 @@ __global__ __launch_bounds__(256) void k_attn_combine(StrideAttentionParams p) {
 // Otherwise the workgroup scans the whole list for its row, sums the listed
 // pages, reads the unlisted pages' records from scratch and stores the records
 // it summed there, as k_attn_page would.
-// Orders one wave's LDS writes before its later LDS reads of other lanes'
-// data without waiting for the rest of the workgroup.
-__device__ __forceinline__ void wave_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
 constexpr int kListMaxPages = 320;  // pages a LIST workgroup tracks (the LDS bound is lower)
 
 template <int D, int NWV, bool LIST>
@@ -467,12 +459,7 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_fused(StrideAttentionParams p
         if (lane == 0) part[wave] = s;
       }
     }
-    // The V rows and weights staged below are this wave's own (vs[wave],
-    // w4[wave]): a wave-local barrier orders them (LDS operations of one wave
-    // complete in order). Round 0 of a LIST launch also publishes part[] to
-    // the other waves, which takes the workgroup barrier.
-    if (LIST && it == 0) __syncthreads();
-    else wave_sync();
+    __syncthreads();  // this wave's V rows
     if constexpr (LIST) {
       if (it == 0) {  // row j's stretch of the list: loads issued now, compared at the end of the round
 #pragma unroll
@@ -526,7 +513,7 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_fused(StrideAttentionParams p
       if (lane < n)
         w4[wave][lane] = f32x4{det_exp(sc[0] - mx[0]), det_exp(sc[1] - mx[1]), det_exp(sc[2] - mx[2]), det_exp(sc[3] - mx[3])};
     }
-    wave_sync();  // this wave's weights
+    __syncthreads();  // this wave's weights
     if (active) {
       float* rec = recs + page * RF;
       const float* wflat = reinterpret_cast<const float*>(w4[wave]);
@@ -552,7 +539,7 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_fused(StrideAttentionParams p
         rec[4 + lane] = dn;
       }
     }
-    wave_sync();  // the staging buffers are reused by the next round
+    __syncthreads();  // the staging buffers are reused by the next round
     if constexpr (LIST) {
       if (it == 0) {
         int ok = list_ok && item_row == j && item_page == t;
@@ -580,7 +567,6 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_fused(StrideAttentionParams p
       }
     }
   }
-  __syncthreads();  // every wave's page records
   if constexpr (LIST) {
     if (!whole) {  // store the summed records, as the page kernel does
       float* dst = p.scratch + static_cast<int64_t>(j * p.n_kv + g) * p.max_pages * p.rec_floats;
