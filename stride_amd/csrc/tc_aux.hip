@@ -523,7 +523,7 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_fused(StrideAttentionParams p
         const int d = lane + 64 * itd;
         if (d >= D) continue;
         f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 4
+#pragma unroll 8
         for (int i = 0; i < n; ++i) {
           const float v = f32_of(static_cast<uint32_t>(vs[wave][i][d]) << 16);
           const f32x4 wi = w4[wave][i];
