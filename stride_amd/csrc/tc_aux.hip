@@ -29,6 +29,31 @@ constexpr int kAttnPageShift = 6;
 constexpr int kAttnPage = 1 << kAttnPageShift;
 constexpr int kHeadsPerGroup = 4;  // the reference's float4 query packing
 
+// Maximum over the 64 lanes of a wave, in registers: DPP within each row of 16
+// lanes (neighbours in a quad, then rotations by 4 and 8), then the row swaps
+// of gfx950 (v_permlane16_swap, v_permlane32_swap; each lane receives its own
+// value or its partner row's in the two results, so both are folded in). Each
+// step keeps the larger of two values (a strict > pick); scores are sums from a
+// +0 start, never -0, so the maximum is the same value whatever the pairing.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float pick_gt(float o, float m) { return o > m ? o : m; }
+__device__ __forceinline__ float wave_max(float m) {
+  m = pick_gt(dpp_f32<0xB1>(m), m);   // quad_perm [1,0,3,2]
+  m = pick_gt(dpp_f32<0x4E>(m), m);   // quad_perm [2,3,0,1]
+  m = pick_gt(dpp_f32<0x124>(m), m);  // row_ror:4
+  m = pick_gt(dpp_f32<0x128>(m), m);  // row_ror:8
+  const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+  m = pick_gt(__uint_as_float(r16[0]), m);
+  m = pick_gt(__uint_as_float(r16[1]), m);
+  const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+  m = pick_gt(__uint_as_float(r32[0]), m);
+  m = pick_gt(__uint_as_float(r32[1]), m);
+  return m;
+}
+
 // ---------------------------------------------------------------------------
 // Embedding: lane j of the h tiles <- fp32(embed row tokens[j]). The embedding
 // is the LM head's weight tiles, so row `token` is slot token % 16 of row tile
@@ -268,13 +293,7 @@ __global__ __launch_bounds__(64) void k_attn_page(StrideAttentionParams p, int p
 #pragma unroll
   for (int h = 0; h < kHeadsPerGroup; ++h) {
     if (lane >= n) sc[h] = neg_inf;
-    float m = sc[h];
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-      const float o = __shfl_xor(m, off);
-      if (o > m) m = o;
-    }
-    mx[h] = m;
+    mx[h] = wave_max(sc[h]);
   }
   if (lane < n) w4[lane] = f32x4{det_exp(sc[0] - mx[0]), det_exp(sc[1] - mx[1]), det_exp(sc[2] - mx[2]), det_exp(sc[3] - mx[3])};
   __syncthreads();
@@ -502,13 +521,7 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_fused(StrideAttentionParams p
 #pragma unroll
       for (int h = 0; h < kHeadsPerGroup; ++h) {
         if (lane >= n) sc[h] = neg_inf;
-        float m = sc[h];
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) {
-          const float o = __shfl_xor(m, off);
-          if (o > m) m = o;
-        }
-        mx[h] = m;
+        mx[h] = wave_max(sc[h]);
       }
       if (lane < n)
         w4[wave][lane] = f32x4{det_exp(sc[0] - mx[0]), det_exp(sc[1] - mx[1]), det_exp(sc[2] - mx[2]), det_exp(sc[3] - mx[3])};
