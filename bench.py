@@ -522,8 +522,8 @@ def engine_step(torch, dev, m, steps, warmup, position=383):
 def exact_step(torch, batches=(1, 32), steps=5):
     """The exact FP32 path end to end on the GPU (stride_amd.exact_engine over the
     stride_k_* kernels, bit-identical to the reference's CPU exact path): one greedy
-    decode step of random-init Llama-3.2-1B with fp32 weights (4.9 GB read per step),
-    host-launched, every row at position 100."""
+    decode step of random-init Llama-3.2-1B (bf16 weights widened to fp32 in the
+    kernels, 2.47 GB read per step), host-launched, every row at position 100."""
     from stride_amd import exact_engine as E
     from stride_amd.weights import ModelConfig
 
