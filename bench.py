@@ -59,7 +59,7 @@ def parse():
                     help="run only the measured steps (host-launched, no graph, no per-op timing; for kernel "
                     "profiles of the step as it is measured) and print its time")
     ap.add_argument("--exact-step", type=int, default=0,
-                    help="time the exact FP32 path's whole decode step (random-init Llama-3.2-1B, fp32 weights, "
+                    help="time the exact FP32 path's whole decode step (random-init Llama-3.2-1B, bf16 weights, "
                     "batch 1 and 32, position 100) and print its JSON")
     ap.add_argument("--summarize-trace", default="",
                     help="print per-kernel launch counts and durations from a rocprofv3 kernel_trace.csv and exit")
