@@ -40,31 +40,62 @@ __device__ __forceinline__ void chain(const uint16_t* wg, const float* x, int st
                                       float (&acc)[4 * J]) {
 #pragma unroll
   for (int e = 0; e < 4 * J; ++e) acc[e] = 0.0f;
-  const int lines = cols / 8;
-  for (int line = t; line < lines; line += kChains) {
+  // Line k's weights (four 16-byte words) and x columns k .. k+7.
+  struct Line {
+    u32x4 v[4];
+    f32x4 xc[J == 1 ? 2 : 8];
+  };
+  auto load = [&](int line, Line& L) {
     const int k = line * 8;
     const u32x4* wl = reinterpret_cast<const u32x4*>(wg + static_cast<int64_t>(k) * 4);
-    const u32x4 v[4] = {wl[0], wl[1], wl[2], wl[3]};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) L.v[q] = wl[q];
+    if constexpr (J == 1) {
+      L.xc[0] = *reinterpret_cast<const f32x4*>(x + k);
+      L.xc[1] = *reinterpret_cast<const f32x4*>(x + k + 4);
+    } else {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) L.xc[c] = *reinterpret_cast<const f32x4*>(x + static_cast<int64_t>(k + c) * stride);
+    }
+  };
+  auto step = [&](const Line& L) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        const int c = k + 2 * q + h;
-        const float w[4] = {lo_half(v[q][2 * h]), hi_half(v[q][2 * h]), lo_half(v[q][2 * h + 1]),
-                            hi_half(v[q][2 * h + 1])};
+        const int c = 2 * q + h;  // column k + c
+        const float w[4] = {lo_half(L.v[q][2 * h]), hi_half(L.v[q][2 * h]), lo_half(L.v[q][2 * h + 1]),
+                            hi_half(L.v[q][2 * h + 1])};
         if constexpr (J == 1) {
-          const float xc = x[c];
+          const float xc = L.xc[c >> 2][c & 3];
 #pragma unroll
           for (int r = 0; r < 4; ++r) acc[r] = __builtin_fmaf(w[r], xc, acc[r]);
         } else {
-          const f32x4 xc = *reinterpret_cast<const f32x4*>(x + static_cast<int64_t>(c) * stride);
 #pragma unroll
           for (int r = 0; r < 4; ++r)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc[r * 4 + j] = __builtin_fmaf(w[r], xc[j], acc[r * 4 + j]);
+            for (int j = 0; j < 4; ++j) acc[r * 4 + j] = __builtin_fmaf(w[r], L.xc[c][j], acc[r * 4 + j]);
         }
       }
     }
+  };
+  // Lines t, t + 32, ... in ascending order, their loads issued NB lines at a
+  // time so that a lane waits one memory round trip per batch, not per line.
+  constexpr int NB = J == 1 ? 4 : 2;
+  const int lines = cols / 8;
+  int line = t;
+  for (; line + (NB - 1) * kChains < lines; line += NB * kChains) {
+    Line L[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) load(line + b * kChains, L[b]);
+    __builtin_amdgcn_sched_barrier(0);  // every load of the batch before the first use
+#pragma unroll
+    for (int b = 0; b < NB; ++b) step(L[b]);
+  }
+  for (; line < lines; line += kChains) {
+    Line L;
+    load(line, L);
+    step(L);
   }
 }
 
