@@ -81,7 +81,7 @@ __device__ __forceinline__ void chain(const uint16_t* wg, const float* x, int st
   };
   // Lines t, t + 32, ... in ascending order, their loads issued NB lines at a
   // time so that a lane waits one memory round trip per batch, not per line.
-  constexpr int NB = J == 1 ? 4 : 2;
+  constexpr int NB = J == 1 ? 8 : 2;
   const int lines = cols / 8;
   int line = t;
   for (; line + (NB - 1) * kChains < lines; line += NB * kChains) {
