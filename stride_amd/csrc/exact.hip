@@ -294,24 +294,46 @@ __global__ __launch_bounds__(64) void k_exact_norm(StrideNormParams p) {
   const int units = p.dim / 4, stride = p.l.stride;
   const float* in = J == 1 ? p.in : p.in + (live ? block : 0) * 4;
   float* out = J == 1 ? p.out : p.out + (live ? block : 0) * 4;
+  // A lane's units u = t, t + 32, ... are loaded NB at a time before their
+  // FMAs, so the chain waits one memory round trip per batch, not per unit.
+  constexpr int NB = J == 1 ? 8 : 4;
+  auto load_unit = [&](int u, f32x4 (&v)[4]) {
+    const int k = u * 4;
+    if constexpr (J == 1) {
+      v[0] = *reinterpret_cast<const f32x4*>(in + k);
+    } else {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) v[c] = *reinterpret_cast<const f32x4*>(in + static_cast<int64_t>(k + c) * stride);
+    }
+  };
   if (live) {
     float acc[J];
 #pragma unroll
     for (int j = 0; j < J; ++j) acc[j] = 0.0f;
-    for (int u = t; u < units; u += kChains) {
-      const int k = u * 4;
+    auto sum_unit = [&](const f32x4 (&v)[4]) {
       if constexpr (J == 1) {
-        const f32x4 v = *reinterpret_cast<const f32x4*>(in + k);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) acc[0] = __builtin_fmaf(v[e], v[e], acc[0]);
+        for (int e = 0; e < 4; ++e) acc[0] = __builtin_fmaf(v[0][e], v[0][e], acc[0]);
       } else {
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const f32x4 v = *reinterpret_cast<const f32x4*>(in + static_cast<int64_t>(k + c) * stride);
+        for (int c = 0; c < 4; ++c)
 #pragma unroll
-          for (int j = 0; j < 4; ++j) acc[j] = __builtin_fmaf(v[j], v[j], acc[j]);
-        }
+          for (int j = 0; j < 4; ++j) acc[j] = __builtin_fmaf(v[c][j], v[c][j], acc[j]);
       }
+    };
+    int u = t;
+    for (; u + (NB - 1) * kChains < units; u += NB * kChains) {
+      f32x4 v[NB][4];
+#pragma unroll
+      for (int b = 0; b < NB; ++b) load_unit(u + b * kChains, v[b]);
+      __builtin_amdgcn_sched_barrier(0);  // every load of the batch before the first FMA
+#pragma unroll
+      for (int b = 0; b < NB; ++b) sum_unit(v[b]);
+    }
+    for (; u < units; u += kChains) {
+      f32x4 v[4];
+      load_unit(u, v);
+      sum_unit(v);
     }
 #pragma unroll
     for (int j = 0; j < J; ++j) part[half][t][j] = acc[j];
@@ -324,27 +346,40 @@ __global__ __launch_bounds__(64) void k_exact_norm(StrideNormParams p) {
   }
   __syncthreads();
   if (!live) return;
-  for (int u = t; u < units; u += kChains) {
+  auto scale_unit = [&](int u, const f32x4& w4, const f32x4 (&v)[4]) {
     const int k = u * 4;
-    const f32x4 w4 = *reinterpret_cast<const f32x4*>(p.weight + k);
     if constexpr (J == 1) {
-      const f32x4 v = *reinterpret_cast<const f32x4*>(in + k);
       const float r = rs[half][0];
       f32x4 o;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) o[e] = w4[e] * (v[e] * r);
+      for (int e = 0; e < 4; ++e) o[e] = w4[e] * (v[0][e] * r);
       *reinterpret_cast<f32x4*>(out + k) = o;
     } else {
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        const int64_t at = static_cast<int64_t>(k + c) * stride;
-        const f32x4 v = *reinterpret_cast<const f32x4*>(in + at);
         f32x4 o;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) o[j] = w4[c] * (v[j] * rs[half][j]);
-        *reinterpret_cast<f32x4*>(out + at) = o;
+        for (int j = 0; j < 4; ++j) o[j] = w4[c] * (v[c][j] * rs[half][j]);
+        *reinterpret_cast<f32x4*>(out + static_cast<int64_t>(k + c) * stride) = o;
       }
     }
+  };
+  int u = t;
+  for (; u + (NB - 1) * kChains < units; u += NB * kChains) {
+    f32x4 v[NB][4], w4[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      w4[b] = *reinterpret_cast<const f32x4*>(p.weight + (u + b * kChains) * 4);
+      load_unit(u + b * kChains, v[b]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int b = 0; b < NB; ++b) scale_unit(u + b * kChains, w4[b], v[b]);
+  }
+  for (; u < units; u += kChains) {
+    f32x4 v[4];
+    load_unit(u, v);
+    scale_unit(u, *reinterpret_cast<const f32x4*>(p.weight + u * 4), v);
   }
 }
 
