@@ -230,15 +230,23 @@ struct QkvOp {  // src/kernels.cu:204-284
   }
 };
 
-// Two reference blocks per 64-lane workgroup: block = 2 * blockIdx.x + half,
-// (weight group, lane group) = (block / lane_groups, block % lane_groups).
+// Two reference blocks per 64-lane workgroup: block = 2 * (logical workgroup) +
+// half, (weight group, lane group) = (block / lane_groups, block % lane_groups).
+// The hardware hands workgroup i to XCD i % 8; logical workgroups are numbered so
+// that consecutive ones (the lane groups of one weight group) share an XCD and
+// so read that group's weights through one L2.
+__device__ __forceinline__ int exact_wg_order(int i, int n) {
+  const int full = n & ~7;
+  if (i >= full) return i;
+  return (i & 7) * (full >> 3) + (i >> 3);
+}
 template <class Op, int J>
 __global__ __launch_bounds__(64) void k_exact_gemm(typename Op::Params p, int nblocks) {
   constexpr int M = Op::kMats;
   __shared__ float part[2][kChains][M][4 * J];
   __shared__ float ys[2][M][16];
   const int half = threadIdx.x >> 5, t = threadIdx.x & 31;
-  const int block = blockIdx.x * 2 + half;
+  const int block = exact_wg_order(blockIdx.x, gridDim.x) * 2 + half;
   const bool live = block < nblocks;
   const int lg = live ? block % p.l.lane_groups : 0;
   const int group = live ? block / p.l.lane_groups : 0;
