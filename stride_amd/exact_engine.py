@@ -222,21 +222,27 @@ class ExactEngine:
         self.items = B.zeros(lanes * self.max_pages * 2, np.int32)
         self.scratch = B.zeros(lanes * cfg.kv_heads * self.max_pages * self.rec_floats, np.float32)
 
-    def step(self, rows, greedy=(), full=()):
-        """One step over rows [(slot, pos, token)]. Returns ([(index, value bits)]
-        for the rows listed in `greedy`, [fp32 logits[vocab]] for those in `full`),
-        both in list order."""
-        cfg, B = self.cfg, self.B
+    def upload(self, rows):
+        """Host part of a step: the rows' tokens, slots, positions and attention
+        items into their device buffers. Returns the item count."""
+        B = self.B
         n = len(rows)
         if not 0 < n <= self.max_rows:
             raise ValueError("step needs 1 .. max_rows rows")
-        J, lg, stride = exact.lane_shape(n)
-        lanes = Lanes(n, lg, stride, 0)
         B.put(self.tokens, np.array([r[2] for r in rows], np.int32))
         B.put(self.row_slot, np.array([r[0] for r in rows], np.int32))
         B.put(self.row_pos, np.array([r[1] for r in rows], np.int32))
         items = np.array([[j, pg] for j, r in enumerate(rows) for pg in range((r[1] >> 6) + 1)], np.int32)
         B.put(self.items, items.reshape(-1))
+        return len(items)
+
+    def launch_layers(self, n, item_count):
+        """Device part of a step up to the final RMSNorm (self.nx), for n uploaded
+        rows: only kernel launches on the current stream, so it can be captured in
+        a HIP graph."""
+        cfg, B = self.cfg, self.B
+        J, lg, stride = exact.lane_shape(n)
+        lanes = Lanes(n, lg, stride, 0)
         H, D = cfg.hidden, cfg.head_dim
         q_stride = cfg.heads * D
         scale = float(math.pow(D, -0.5))
@@ -251,7 +257,7 @@ class ExactEngine:
             a.l = lanes
             a.q, a.q_stride, a.out, a.out_cols = P(self.q), q_stride, P(self.attn), q_stride
             a.kv = self.kv
-            a.row_slot, a.row_pos, a.items, a.item_count = P(self.row_slot), P(self.row_pos), P(self.items), len(items)
+            a.row_slot, a.row_pos, a.items, a.item_count = P(self.row_slot), P(self.row_pos), P(self.items), item_count
             a.scratch, a.max_pages, a.rec_floats = P(self.scratch), self.max_pages, self.rec_floats
             a.layer, a.n_kv, a.n_q, a.head_dim, a.scale = li, cfg.kv_heads, cfg.repeat(), D, scale
             B.call("attention", a)
@@ -260,6 +266,25 @@ class ExactEngine:
             B.call("mlp13", Mlp13Params(lanes, P(self.nx), m["w1"], m["w3"], P(self.z)), J)
             B.call("gemm_residual", GemmResidualParams(lanes, P(self.z), m["w2"], P(self.h)), J)
         B.call("norm", NormParams(lanes, P(self.h), P(self.nx), P(self.norm_final), H, cfg.rms_eps), J)
+        return J, lanes
+
+    def launch_lm_greedy_all(self, n):
+        """The greedy LM head over all n rows in lane order (self.nx), writing
+        self.best; the caller initialises self.best to (-inf, -1) per row."""
+        cJ, clg, cstride = exact.lane_shape(n)
+        self.B.call("lm_greedy", LmGreedyParams(Lanes(n, clg, cstride, 0), self.B.ptr(self.nx), self.lm_mat,
+                                                self.cfg.vocab, self.B.ptr(self.best)), cJ)
+
+    def step(self, rows, greedy=(), full=()):
+        """One step over rows [(slot, pos, token)]. Returns ([(index, value bits)]
+        for the rows listed in `greedy`, [fp32 logits[vocab]] for those in `full`),
+        both in list order."""
+        cfg, B = self.cfg, self.B
+        n = len(rows)
+        item_count = self.upload(rows)
+        J, lanes = self.launch_layers(n, item_count)
+        H = cfg.hidden
+        P = B.ptr
 
         def lm_input(wanted):
             """Lane shape of the wanted rows and the activations holding them in
