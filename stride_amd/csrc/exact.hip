@@ -30,20 +30,23 @@ __device__ __forceinline__ float lo_half(uint32_t v) { return f32_of(v << 16); }
 __device__ __forceinline__ float hi_half(uint32_t v) { return f32_of(v & 0xFFFF0000u); }
 
 // Chain t of the dot products of one four-row weight group (wg: [col][4] bf16)
-// with J lanes of x (dim-major, lane j of column c at x[c * stride + j]):
-// acc[r * J + j] for row r, lane j. Lines of 8 columns: t, t + 32, ...; each
-// line is four 16-byte words, word q holding columns k + 2q (rows 0-3 in its
-// first two 32-bit halves' bf16 pairs) and k + 2q + 1 (last two)
-// (src/kernels.cu:22-94).
-template <int J>
+// with LG lane groups of J lanes of x (dim-major, lane j of column c at
+// x[c * stride + j], lane group i at x + 4 * xi[i]): acc[(i * 4 + r) * J + j] for
+// lane group i, row r, lane j. Lines of 8 columns: t, t + 32, ...; each line is
+// four 16-byte words, word q holding columns k + 2q (rows 0-3 in its first two
+// 32-bit halves' bf16 pairs) and k + 2q + 1 (last two) (src/kernels.cu:22-94).
+// A weight line is loaded once for the LG lane groups; every output's FMAs run
+// in the same order whatever LG is.
+template <int J, int LG>
 __device__ __forceinline__ void chain(const uint16_t* wg, const float* x, int stride, int cols, int t,
-                                      float (&acc)[4 * J]) {
+                                      const int (&xi)[LG], float (&acc)[4 * J * LG]) {
+  static_assert(J == 4 || LG == 1, "one lane: one lane group");
 #pragma unroll
-  for (int e = 0; e < 4 * J; ++e) acc[e] = 0.0f;
-  // Line k's weights (four 16-byte words) and x columns k .. k+7.
+  for (int e = 0; e < 4 * J * LG; ++e) acc[e] = 0.0f;
+  // Line k's weights (four 16-byte words) and x columns k .. k+7 of each lane group.
   struct Line {
     u32x4 v[4];
-    f32x4 xc[J == 1 ? 2 : 8];
+    f32x4 xc[LG][J == 1 ? 2 : 8];
   };
   auto load = [&](int line, Line& L) {
     const int k = line * 8;
@@ -51,11 +54,14 @@ __device__ __forceinline__ void chain(const uint16_t* wg, const float* x, int st
 #pragma unroll
     for (int q = 0; q < 4; ++q) L.v[q] = wl[q];
     if constexpr (J == 1) {
-      L.xc[0] = *reinterpret_cast<const f32x4*>(x + k);
-      L.xc[1] = *reinterpret_cast<const f32x4*>(x + k + 4);
+      L.xc[0][0] = *reinterpret_cast<const f32x4*>(x + k);
+      L.xc[0][1] = *reinterpret_cast<const f32x4*>(x + k + 4);
     } else {
 #pragma unroll
-      for (int c = 0; c < 8; ++c) L.xc[c] = *reinterpret_cast<const f32x4*>(x + static_cast<int64_t>(k + c) * stride);
+      for (int i = 0; i < LG; ++i)
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
+          L.xc[i][c] = *reinterpret_cast<const f32x4*>(x + static_cast<int64_t>(k + c) * stride + 4 * xi[i]);
     }
   };
   auto step = [&](const Line& L) {
@@ -67,21 +73,24 @@ __device__ __forceinline__ void chain(const uint16_t* wg, const float* x, int st
         const float w[4] = {lo_half(L.v[q][2 * h]), hi_half(L.v[q][2 * h]), lo_half(L.v[q][2 * h + 1]),
                             hi_half(L.v[q][2 * h + 1])};
         if constexpr (J == 1) {
-          const float xc = L.xc[c >> 2][c & 3];
+          const float xc = L.xc[0][c >> 2][c & 3];
 #pragma unroll
           for (int r = 0; r < 4; ++r) acc[r] = __builtin_fmaf(w[r], xc, acc[r]);
         } else {
 #pragma unroll
-          for (int r = 0; r < 4; ++r)
+          for (int i = 0; i < LG; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc[r * 4 + j] = __builtin_fmaf(w[r], L.xc[c][j], acc[r * 4 + j]);
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+              for (int j = 0; j < 4; ++j)
+                acc[(i * 4 + r) * 4 + j] = __builtin_fmaf(w[r], L.xc[i][c][j], acc[(i * 4 + r) * 4 + j]);
         }
       }
     }
   };
   // Lines t, t + 32, ... in ascending order, their loads issued NB lines at a
   // time so that a lane waits one memory round trip per batch, not per line.
-  constexpr int NB = J == 1 ? 8 : 2;
+  constexpr int NB = J == 1 ? 8 : (LG <= 2 ? 2 : 1);
   const int lines = cols / 8;
   int line = t;
   for (; line + (NB - 1) * kChains < lines; line += NB * kChains) {
@@ -230,49 +239,61 @@ struct QkvOp {  // src/kernels.cu:204-284
   }
 };
 
-// Two reference blocks per 64-lane workgroup: block = 2 * (logical workgroup) +
-// half, (weight group, lane group) = (block / lane_groups, block % lane_groups).
-// The hardware hands workgroup i to XCD i % 8; logical workgroups are numbered so
-// that consecutive ones (the lane groups of one weight group) share an XCD and
-// so read that group's weights through one L2.
+// Two blocks per 64-lane workgroup: block = 2 * (logical workgroup) + half. A
+// block is one reference block (one weight group, one lane group) for LG = 1, or
+// the reference blocks of one weight group and LG consecutive lane groups, which
+// then share each weight line load: (weight group, lane-group set) = (block /
+// sets, block % sets). The hardware hands workgroup i to XCD i % 8; logical
+// workgroups are numbered so that consecutive ones (the lane groups of one
+// weight group) share an XCD and so read that group's weights through one L2.
 __device__ __forceinline__ int exact_wg_order(int i, int n) {
   const int full = n & ~7;
   if (i >= full) return i;
   return (i & 7) * (full >> 3) + (i >> 3);
 }
-template <class Op, int J>
+
+template <class Op, int J, int LG>
 __global__ __launch_bounds__(64) void k_exact_gemm(typename Op::Params p, int nblocks) {
   constexpr int M = Op::kMats;
-  __shared__ float part[2][kChains][M][4 * J];
-  __shared__ float ys[2][M][16];
+  constexpr int NO = 4 * J;  // outputs per reference block
+  __shared__ float part[2][kChains][M][NO * LG];
+  __shared__ float ys[2][LG][M][16];
   const int half = threadIdx.x >> 5, t = threadIdx.x & 31;
   const int block = exact_wg_order(blockIdx.x, gridDim.x) * 2 + half;
   const bool live = block < nblocks;
-  const int lg = live ? block % p.l.lane_groups : 0;
-  const int group = live ? block / p.l.lane_groups : 0;
+  const int sets = (p.l.lane_groups + LG - 1) / LG;
+  const int set = live ? block % sets : 0;
+  const int group = live ? block / sets : 0;
+  const int lg0 = set * LG, nlg = min(LG, p.l.lane_groups - lg0);
   if (live) {
-    const float* x = J == 1 ? p.x : p.x + lg * 4;
+    const float* x = J == 1 ? p.x : p.x + lg0 * 4;
+    int xi[LG];  // lane groups past the last live one read the last live one's x
+#pragma unroll
+    for (int i = 0; i < LG; ++i) xi[i] = min(i, nlg - 1);
 #pragma unroll
     for (int m = 0; m < M; ++m) {
       int cols = 0;
       const uint16_t* wg = Op::w(p, m, group, cols);
-      float acc[4 * J];
-      chain<J>(wg, x, p.l.stride, cols, t, acc);
+      float acc[NO * LG];
+      chain<J, LG>(wg, x, p.l.stride, cols, t, xi, acc);
 #pragma unroll
-      for (int e = 0; e < 4 * J; ++e) part[half][t][m][e] = acc[e];
+      for (int e = 0; e < NO * LG; ++e) part[half][t][m][e] = acc[e];
     }
   }
   __syncthreads();
-  if (live && t < 4 * J) {
+  if (live) {
+    for (int e = t; e < NO * LG; e += kChains) {
 #pragma unroll
-    for (int m = 0; m < M; ++m) {
-      float y = part[half][0][m][t];
-      for (int i = 1; i < kChains; ++i) y = y + part[half][i][m][t];
-      ys[half][m][t] = y;
+      for (int m = 0; m < M; ++m) {
+        float y = part[half][0][m][e];
+        for (int i = 1; i < kChains; ++i) y = y + part[half][i][m][e];
+        ys[half][e / NO][m][e % NO] = y;
+      }
     }
   }
   __syncthreads();
-  if (live) Op::template finish<J>(p, group, lg, t, ys[half]);
+  if (live)
+    for (int i = 0; i < nlg; ++i) Op::template finish<J>(p, group, lg0 + i, t, ys[half][i]);
 }
 
 // ---------------------------------------------------------------------------
@@ -423,14 +444,19 @@ int launched(const char* what) {
   return 0;
 }
 
+#ifndef STRIDE_EXACT_LG
+#define STRIDE_EXACT_LG 2
+#endif
 template <class Op>
 int run_gemm(const typename Op::Params& p, int J, void* stream, const char* what) {
-  const int nblocks = Op::groups(p) * p.l.lane_groups;
+  constexpr int LG = STRIDE_EXACT_LG;  // lane groups sharing a weight line load
+  const int lg = J == 1 ? 1 : LG;
+  const int nblocks = Op::groups(p) * ((p.l.lane_groups + lg - 1) / lg);
   if (p.l.rows == 0 || nblocks == 0) return 0;
   const dim3 grid((nblocks + 1) / 2);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (J == 1) hipLaunchKernelGGL((k_exact_gemm<Op, 1>), grid, dim3(64), 0, st, p, nblocks);
-  else hipLaunchKernelGGL((k_exact_gemm<Op, 4>), grid, dim3(64), 0, st, p, nblocks);
+  if (J == 1) hipLaunchKernelGGL((k_exact_gemm<Op, 1, 1>), grid, dim3(64), 0, st, p, nblocks);
+  else hipLaunchKernelGGL((k_exact_gemm<Op, 4, LG>), grid, dim3(64), 0, st, p, nblocks);
   return launched(what);
 }
 
