@@ -48,13 +48,6 @@ __device__ __forceinline__ int xs_unit0(const Geometry& g, int si) {
   return u;
 }
 
-// Finish of a cross-workgroup split launch (one split per workgroup). With a
-// single split the tiles are final. Otherwise every workgroup of a (row block,
-// lane group) unit publishes its partial tiles with device-coherent stores and
-// counts itself in at `cnt`; the last one to arrive folds the splits in
-// ascending order, y = ((c0 + c1) + c2) + ..., applies the epilogue and re-arms
-// the counter for the next launch. Nothing waits on another workgroup. Rows
-// rt_first .. rt_first+R-1 and lane tiles lt0 .. lt0+nlt-1 are this wave's.
 // Fold of the last arriving workgroup of a cross-workgroup split unit, for a
 // split count S known at compile time. Every split's partial tile is loaded back
 // (its own too: it was stored before the arrival count, and the copy is
@@ -113,6 +106,13 @@ __device__ __forceinline__ void xs_fold(const Geometry& g, const typename Epi::O
   });
 }
 
+// Finish of a cross-workgroup split launch (one split per workgroup). With a
+// single split the tiles are final. Otherwise every workgroup of a (row block,
+// lane group) unit publishes its partial tiles with device-coherent stores and
+// counts itself in at `cnt`; the last one to arrive folds the splits in
+// ascending order, y = ((c0 + c1) + c2) + ..., applies the epilogue and re-arms
+// the counter for the next launch. Nothing waits on another workgroup. Rows
+// rt_first .. rt_first+R-1 and lane tiles lt0 .. lt0+nlt-1 are this wave's.
 template <class Epi, int R, int LT>
 __device__ __forceinline__ void xs_finish(const Geometry& g, const typename Epi::Out& o, int si, const Segment& sg,
                                           int rt_first, int lt0, int nlt, int* cnt, int splits, int my_split,
