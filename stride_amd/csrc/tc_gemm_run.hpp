@@ -572,11 +572,11 @@ inline Pick pick_small(int T, int smax, int mats, int nseg, int per) {
     return {3, 31};
   }
   if (smax == 4) {  // the split rule's few-row matrices; per = chunks per split (down: 64, O and QKV: 16)
-    // QKV: 6.3 / 7.0 / 8.3 / 9.3 us at M = 1 / 32 / 64 / 128. From five lane tiles the
+    // QKV: 5.7 / 6.5 / 7.9 / 9.3 us at M = 1 / 32 / 64 / 128. From five lane tiles the
     // flat row blocks of three row tiles (straddling the Q/K/V boundaries) fill all
     // 256 CUs with 64 x 4 workgroups (9.3 against 9.7 us for 2-tile blocks at M = 128).
     if (nseg == 3) return {0, T <= 1 ? 0 : (T <= 2 ? 5 : (T <= 4 ? 33 : 60))};
-    if (per >= 32) {  // down: 11.2 / 11.9 / 14.5 / 15.9 us at M = 1 / 32 / 64 / 128
+    if (per >= 32) {  // down: 10.3 / 11.6 / 13.8 / 15.7 us at M = 1 / 32 / 64 / 128
       if (T <= 1) return {0, 55};
       // Two lane tiles, two waves, one split per workgroup: 1.5-3 % faster decode
       // steps at M = 32-64 than the streaming kernel (configurations 0 and 5).
