@@ -31,7 +31,11 @@ def setup():
 
     W = dict(o=w(2048, 2048), o_odd=w(592, 2048), down=w(512, 8192), w1=w(1024, 2048), w3=w(1024, 2048), w1b=w(8192, 2048), w3b=w(8192, 2048), lm=w(4000, 2048), lm1=w(16400, 2048),
              q=w(512, 2048, layout.rope_rows(512, 64)), k=w(128, 2048, layout.rope_rows(128, 64)),
-             v=w(128, 2048, layout.rope_rows(128, 64)))
+             v=w(128, 2048, layout.rope_rows(128, 64)),
+             # 20 + 4 + 4 row tiles: three-tile flat blocks straddle the Q/K boundary
+             # and the last block is partial
+             q5=w(320, 2048, layout.rope_rows(320, 64)), k1=w(64, 2048, layout.rope_rows(64, 64)),
+             v1=w(64, 2048, layout.rope_rows(64, 64)))
     x = {k: (torch.randn(128, k, generator=g, device=DEV)).to(torch.bfloat16).view(torch.int16) for k in (2048, 8192)}
     h = torch.randn(128, 2048, generator=g, device=DEV)
     W["rope"] = torch.rand(17, 32, 2, generator=g, device=DEV)
@@ -62,6 +66,10 @@ def run_all(W, x, h, m):
     q = harness.qkv(W["q"], W["k"], W["v"], xt, m, 64, rope, torch.arange(m, dtype=torch.int32, device=DEV),
                     torch.full((m,), 5, dtype=torch.int32, device=DEV), kv)
     out["qkv"] = digest(q) + digest(kv.arena)
+    kv1 = harness.PagedKv.create(m, 16, 1, 64, 1, 16, DEV)
+    q1 = harness.qkv(W["q5"], W["k1"], W["v1"], xt, m, 64, rope, torch.arange(m, dtype=torch.int32, device=DEV),
+                     torch.full((m,), 5, dtype=torch.int32, device=DEV), kv1)
+    out["qkv_odd"] = digest(q1) + digest(kv1.arena)
     return out
 
 
