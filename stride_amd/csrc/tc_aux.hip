@@ -118,10 +118,17 @@ __global__ __launch_bounds__(64) void k_norm(StrideTcNormParams p, int per_lane)
     }
     return;
   }
-  __shared__ float partial[32];
-  __shared__ float rs;
+  // The 32 lane partials added left to right, ((p0 + p1) + p2) + ..., from
+  // registers (every lane forms the same sum), then r = 1 / sqrt(sum / dim + eps).
+  auto inv_rms = [&](float acc) {
+    float sum = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), 0));
+#pragma unroll
+    for (int i = 1; i < 32; ++i) sum = sum + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), i));
+    return 1.0f / sqrtf(sum / static_cast<float>(p.dim) + p.eps);
+  };
   if constexpr (TPL > 0) {
     f32x4 v[TPL][4], g[TPL][4];
+    float acc = 0.0f;
     if (lane < 32) {
 #pragma unroll
       for (int k = 0; k < TPL; ++k) {
@@ -133,30 +140,21 @@ __global__ __launch_bounds__(64) void k_norm(StrideTcNormParams p, int per_lane)
           g[k][q] = gs[q];
         }
       }
-      float acc = 0.0f;
 #pragma unroll
       for (int k = 0; k < TPL; ++k)
 #pragma unroll
         for (int q = 0; q < 4; ++q)
 #pragma unroll
           for (int c = 0; c < 4; ++c) acc = __builtin_fmaf(v[k][q][c], v[k][q][c], acc);
-      partial[lane] = acc;
     }
-    __syncthreads();
-    if (lane == 0) {
-      float sum = partial[0];
-      for (int i = 1; i < 32; ++i) sum = sum + partial[i];
-      rs = 1.0f / sqrtf(sum / static_cast<float>(p.dim) + p.eps);
-    }
-    __syncthreads();
+    const float r = inv_rms(acc);
     if (lane < 32) {
-      const float r = rs;
 #pragma unroll
       for (int k = 0; k < TPL; ++k) store(lane + 32 * k, v[k], g[k], r);
     }
   } else {
+    float acc = 0.0f;
     if (lane < 32) {
-      float acc = 0.0f;
       for (int ct = lane; ct < col_tiles; ct += 32) {
         const f32x4* v = reinterpret_cast<const f32x4*>(p.h + tile(ct));
 #pragma unroll
@@ -166,16 +164,8 @@ __global__ __launch_bounds__(64) void k_norm(StrideTcNormParams p, int per_lane)
           for (int c = 0; c < 4; ++c) acc = __builtin_fmaf(w[c], w[c], acc);
         }
       }
-      partial[lane] = acc;
     }
-    __syncthreads();
-    if (lane == 0) {
-      float sum = partial[0];
-      for (int i = 1; i < 32; ++i) sum = sum + partial[i];
-      rs = 1.0f / sqrtf(sum / static_cast<float>(p.dim) + p.eps);
-    }
-    __syncthreads();
-    const float r = rs;
+    const float r = inv_rms(acc);
     for (int ct = lane; ct < col_tiles; ct += 64) {
       const f32x4* v = reinterpret_cast<const f32x4*>(p.h + tile(ct));
       const f32x4* gv = reinterpret_cast<const f32x4*>(p.weight + ct * 16);
