@@ -224,7 +224,12 @@ __global__ __launch_bounds__(kWave * WS * WR) void k_stream(Geometry g, typename
   constexpr int U = U0 < UMAX ? U0 : UMAX;
   // x staging needs each batch to split evenly over the row waves of a split group.
   constexpr bool XL = XLC && (U * LT) % WR == 0;
-  constexpr int kY = WS > 1 ? WR * M * R * LT * kWave : 1;           // combine buffer (f32x4 slots)
+  constexpr int kY1 = WR * M * R * LT * kWave;                       // one split's tiles (f32x4 slots)
+  // The split partials get a slot each when they fit in 64 KiB: one barrier, then
+  // each tile's owner adds them in split order. Otherwise one buffer, the splits
+  // adding in turn with a barrier after each.
+  constexpr bool kSplitSlots = WS > 1 && !Epi::kReduce && WS * kY1 * 16 <= 64 * 1024;
+  constexpr int kY = WS > 1 ? (kSplitSlots ? WS * kY1 : kY1) : 1;      // combine buffer (f32x4 slots)
   constexpr int kX = XL ? WS * 2 * U * LT * kWave : 1;                // x staging (u32x4 slots)
   constexpr int kXPieces = U * LT * kWave;                            // 16-byte pieces per x batch
   constexpr int kXPer = XL ? kXPieces / (WR * kWave) : 1;
@@ -541,19 +546,31 @@ __global__ __launch_bounds__(kWave * WS * WR) void k_stream(Geometry g, typename
     }
   } else {
     // Ordered combine: y = c0, then y = y + c1, y = y + c2, ...
-    for (int s = 0; s < splits; ++s) {
-      if (ws == s) {
+    if constexpr (kSplitSlots) {
+      if (ws < splits) {
 #pragma unroll
         for (int m = 0; m < M; ++m)
 #pragma unroll
           for (int r = 0; r < R; ++r)
 #pragma unroll
-            for (int l = 0; l < LT; ++l) {
-              f32x4& y = ybuf[(((wr * M + m) * R + r) * LT + l) * kWave + lane];
-              y = s == 0 ? acc[m][r][l] : y + acc[m][r][l];
-            }
+            for (int l = 0; l < LT; ++l) ybuf[ws * kY1 + (((wr * M + m) * R + r) * LT + l) * kWave + lane] = acc[m][r][l];
       }
       __syncthreads();
+    } else {
+      for (int s = 0; s < splits; ++s) {
+        if (ws == s) {
+#pragma unroll
+          for (int m = 0; m < M; ++m)
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+              for (int l = 0; l < LT; ++l) {
+                f32x4& y = ybuf[(((wr * M + m) * R + r) * LT + l) * kWave + lane];
+                y = s == 0 ? acc[m][r][l] : y + acc[m][r][l];
+              }
+        }
+        __syncthreads();
+      }
     }
     for (int t = wave; t < WR * R * LT; t += WS * WR) {
       const int twr = t / (R * LT), r = (t / LT) % R, l = t % LT;
@@ -561,8 +578,16 @@ __global__ __launch_bounds__(kWave * WS * WR) void k_stream(Geometry g, typename
       if (l >= nlt || rt >= total) continue;
       if constexpr (FLAT) ts = flat_segment(g, rb * (WR * R) + twr * R + r, rt);
       f32x4 y[M];
+      const int at = (((twr * M) * R + r) * LT + l) * kWave + lane;
 #pragma unroll
-      for (int m = 0; m < M; ++m) y[m] = ybuf[(((twr * M + m) * R + r) * LT + l) * kWave + lane];
+      for (int m = 0; m < M; ++m) {
+        if constexpr (kSplitSlots) {
+          y[m] = ybuf[at + m * R * LT * kWave];
+          for (int s = 1; s < splits; ++s) y[m] = y[m] + ybuf[s * kY1 + at + m * R * LT * kWave];
+        } else {
+          y[m] = ybuf[at + m * R * LT * kWave];
+        }
+      }
       Epi::apply(o, g, ts, rt, lt0 + l, y, lane);
     }
   }
