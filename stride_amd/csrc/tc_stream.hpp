@@ -418,24 +418,34 @@ __global__ __launch_bounds__(kWave * WS * WR) void k_stream(Geometry g, typename
     }
   } else {
     if (nbatch > 0) {
+      // Batch b's loads go out while batch b - 1 is multiplied. The loop body
+      // runs while two more batches remain, so its loads are unconditional (a
+      // load behind a branch makes the compiler's wait before the next MFMAs
+      // assume the path without it), and a scheduling barrier keeps each batch's
+      // loads ahead of the previous batch's MFMAs.
       load_w(a0, c0);
       load_x(b0, c0);
       int c = c0;
-      for (;;) {
-        if (c + U < cb) {
-          load_w(a1, c + U);
-          load_x(b1, c + U);
-        }
+      for (; c + 2 * U < cb; c += 2 * U) {
+        load_w(a1, c + U);
+        load_x(b1, c + U);
+        __builtin_amdgcn_sched_barrier(0);
         mma(a0, b0, 0);
-        c += U;
-        if (c >= cb) break;
-        if (c + U < cb) {
-          load_w(a0, c + U);
-          load_x(b0, c + U);
-        }
+        __builtin_amdgcn_sched_barrier(0);
+        load_w(a0, c + 2 * U);
+        load_x(b0, c + 2 * U);
+        __builtin_amdgcn_sched_barrier(0);
         mma(a1, b1, 0);
-        c += U;
-        if (c >= cb) break;
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (c + U < cb) {
+        load_w(a1, c + U);
+        load_x(b1, c + U);
+        __builtin_amdgcn_sched_barrier(0);
+        mma(a0, b0, 0);
+        mma(a1, b1, 0);
+      } else {
+        mma(a0, b0, 0);
       }
     }
     for (int c = cb; c < c1; ++c) {  // tail when U does not divide the split
