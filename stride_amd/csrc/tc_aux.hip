@@ -368,7 +368,9 @@ __global__ __launch_bounds__(256) void k_attn_combine(StrideAttentionParams p) {
 // exactly as k_attn_page does (the same expressions in the same order) into a
 // record kept in LDS; after a barrier the workgroup combines the records in
 // ascending page order exactly as k_attn_combine does and writes the bf16 x
-// tiles. No second launch is needed.
+// tiles (KvT = uint16_t: bf16 KV, the tensor-core path) or the fp32 dim-major
+// output (KvT = float, kExact: the exact path's fp32 KV). No second launch is
+// needed.
 //
 // LIST = false: item_count == -1, every page of every row is computed.
 // LIST = true: the caller's (row, page) item list decides, with the semantics of
@@ -383,15 +385,15 @@ __global__ __launch_bounds__(256) void k_attn_combine(StrideAttentionParams p) {
 // it summed there, as k_attn_page would.
 constexpr int kListMaxPages = 320;  // pages a LIST workgroup tracks (the LDS bound is lower)
 
-template <int D, int NWV, bool LIST>
+template <int D, int NWV, bool LIST, class KvT = uint16_t, bool kExact = false>
 __global__ __launch_bounds__(64 * NWV) void k_attn_fused(StrideAttentionParams p, int page_shift) {
-  constexpr int kEl = 8;                        // bf16 elements per 16-byte piece
+  constexpr int kEl = 16 / static_cast<int>(sizeof(KvT));  // KV elements per 16-byte piece
   constexpr int kPer = kAttnPage * D / kEl / 64;  // V pieces per lane
   constexpr int kKey = D / kEl;                 // 16-byte pieces of one K row
   constexpr int RF = 8 + kHeadsPerGroup * D;    // record floats
   extern __shared__ float recs[];  // [max_pages][RF], f[4][max_pages], then the row's KV page numbers
   __shared__ f32x4 w4[NWV][kAttnPage];
-  __shared__ uint16_t vs[NWV][kAttnPage][D];
+  __shared__ KvT vs[NWV][kAttnPage][D];
   __shared__ uint32_t listed[LIST ? kListMaxPages / 32 : 1];
   __shared__ int part[NWV];
   const int j = blockIdx.x / p.n_kv;
@@ -408,7 +410,7 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_fused(StrideAttentionParams p
   int32_t* btab = reinterpret_cast<int32_t*>(recs + p.max_pages * (RF + kHeadsPerGroup));
   const int nblk = min((last >> page_shift) + 1, (p.max_pages * kAttnPage + (1 << page_shift) - 1) >> page_shift);
   for (int i = t; i < nblk; i += 64 * NWV) btab[i] = p.kv.table[static_cast<int64_t>(slot) * p.kv.max_blocks + i];
-  const uint16_t* kv_base = static_cast<const uint16_t*>(p.kv.arena) + p.layer * p.kv.layer_elems + g * p.kv.group_elems;
+  const KvT* kv_base = static_cast<const KvT*>(p.kv.arena) + p.layer * p.kv.layer_elems + g * p.kv.group_elems;
   auto kv_at = [&](int which, int pos) {
     return kv_base + btab[pos >> page_shift] * p.kv.block_elems + which * p.kv.which_elems +
            static_cast<int64_t>(pos & ((1 << page_shift) - 1)) * D;
@@ -431,7 +433,7 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_fused(StrideAttentionParams p
       const int P = k * 64 + lane, i = P / (D / kEl), c = P % (D / kEl);
       vr[k] = ld_kv(kv_at(1, min(p0 + i, last)) + c * kEl);
     }
-    const uint16_t* key = kv_at(0, min(p0 + lane, last));
+    const KvT* key = kv_at(0, min(p0 + lane, last));
 #pragma unroll
     for (int c = 0; c < kKey; ++c) kr[c] = load16(key + kEl * c);
   };
@@ -491,7 +493,9 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_fused(StrideAttentionParams p
       for (int c = 0; c < kKey; ++c) {
 #pragma unroll
         for (int e = 0; e < kEl; ++e) {
-          const float k = f32_of(e & 1 ? kr[c][e >> 1] & 0xFFFF0000u : kr[c][e >> 1] << 16);
+          float k;
+          if constexpr (kEl == 8) k = f32_of(e & 1 ? kr[c][e >> 1] & 0xFFFF0000u : kr[c][e >> 1] << 16);
+          else k = f32_of(kr[c][e]);
           const int d = kEl * c + e;
           const f32x4 qd = f32x4{cq[d], cq[D + d], cq[2 * D + d], cq[3 * D + d]};
           a0 = __builtin_fmaf(qd[0], k, a0);
@@ -528,7 +532,9 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_fused(StrideAttentionParams p
         f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll 8
         for (int i = 0; i < n; ++i) {
-          const float v = f32_of(static_cast<uint32_t>(vs[wave][i][d]) << 16);
+          float v;
+          if constexpr (kEl == 8) v = f32_of(static_cast<uint32_t>(vs[wave][i][d]) << 16);
+          else v = vs[wave][i][d];
           const f32x4 wi = w4[wave][i];
 #pragma unroll
           for (int h = 0; h < kHeadsPerGroup; ++h) acc[h] = __builtin_fmaf(wi[h], v, acc[h]);
@@ -596,7 +602,7 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_fused(StrideAttentionParams p
   __syncthreads();
   const int col_tiles = p.out_cols >> 4;
   uint16_t* out = static_cast<uint16_t*>(p.out);
-  const int64_t lane0 = static_cast<int64_t>(j >> 4) * col_tiles * kTileElems + (j & 15) * 16;
+  const int64_t lane0 = kExact ? 0 : static_cast<int64_t>(j >> 4) * col_tiles * kTileElems + (j & 15) * 16;
   for (int hd = t; hd < kHeadsPerGroup * D; hd += 64 * NWV) {
     const int qh = hd / D, d = hd % D;
     float acc = 0.0f, dn = 0.0f;
@@ -606,7 +612,8 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_fused(StrideAttentionParams p
       acc = __builtin_fmaf(e, recs[c * RF + 8 + qh * D + d], acc);
     }
     const int idx = (g * kHeadsPerGroup + qh) * D + d;
-    out[lane0 + static_cast<int64_t>(idx >> 4) * kTileElems + (idx & 15)] = static_cast<uint16_t>(bf16_rne(acc / dn));
+    if constexpr (kExact) static_cast<float*>(p.out)[static_cast<int64_t>(idx) * p.l.stride + j] = acc / dn;
+    else out[lane0 + static_cast<int64_t>(idx >> 4) * kTileElems + (idx & 15)] = static_cast<uint16_t>(bf16_rne(acc / dn));
   }
 }
 
@@ -645,23 +652,23 @@ static int combine(dim3 grid, size_t lds, hipStream_t st, const StrideAttentionP
 
 // One-kernel attention; its static LDS (staging for up to four waves) and the
 // row's records share the 160 KiB.
-template <int D, int NWV>
+template <int D, int NWV, class KvT>
 constexpr size_t fused_static_lds() {
-  return NWV * 64 * 16 + NWV * 64 * D * 2 + kListMaxPages / 8 + 4 * NWV;
+  return NWV * 64 * 16 + NWV * 64 * D * sizeof(KvT) + kListMaxPages / 8 + 4 * NWV;
 }
 
-template <int D, int NWV, bool LIST>
+template <int D, int NWV, bool LIST, class KvT, bool kExact>
 static int fused_nwv(dim3 grid, size_t lds, hipStream_t st, const StrideAttentionParams& p, int page_shift) {
-  if (lds + fused_static_lds<D, NWV>() > kCombineLdsMax)
+  if (lds + fused_static_lds<D, NWV, KvT>() > kCombineLdsMax)
     return fail(STRIDE_TC_EINVAL, "tc_attention: max_pages too large for the one-kernel form (use an item list)");
   static size_t raised = 64 * 1024;
   if (lds > raised) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn_fused<D, NWV, LIST>),
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn_fused<D, NWV, LIST, KvT, kExact>),
                                              hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
     if (e != hipSuccess) return fail(static_cast<int>(e), std::string("tc_attention: raising the LDS limit failed: ") + hipGetErrorString(e));
     raised = lds;
   }
-  hipLaunchKernelGGL((k_attn_fused<D, NWV, LIST>), grid, dim3(64 * NWV), lds, st, p, page_shift);
+  hipLaunchKernelGGL((k_attn_fused<D, NWV, LIST, KvT, kExact>), grid, dim3(64 * NWV), lds, st, p, page_shift);
   return launched("attention (one kernel)");
 }
 
@@ -670,17 +677,17 @@ static int fused_nwv(dim3 grid, size_t lds, hipStream_t st, const StrideAttentio
 // workgroups (batch 128, 1024 of them) two waves per workgroup (three rounds of
 // pages) measured best (30.9 us against 32.4 with three and 33+ with four); with
 // fewer (batch 64) four waves finish a row sooner.
-template <int D, bool LIST>
+template <int D, bool LIST, class KvT = uint16_t, bool kExact = false>
 static int fused(dim3 grid, size_t lds, hipStream_t st, const StrideAttentionParams& p, int page_shift) {
-  if (grid.x >= 768) return fused_nwv<D, 2, LIST>(grid, lds, st, p, page_shift);
-  return fused_nwv<D, 4, LIST>(grid, lds, st, p, page_shift);
+  if (grid.x >= 768) return fused_nwv<D, 2, LIST, KvT, kExact>(grid, lds, st, p, page_shift);
+  return fused_nwv<D, 4, LIST, KvT, kExact>(grid, lds, st, p, page_shift);
 }
 
 // Does the one-kernel form serve a call with this dynamic LDS? (4 waves: the
 // larger static staging.)
-template <int D>
+template <int D, class KvT = uint16_t>
 static bool fused_fits(size_t lds) {
-  return lds + fused_static_lds<D, 4>() <= kCombineLdsMax;
+  return lds + fused_static_lds<D, 4, KvT>() <= kCombineLdsMax;
 }
 
 // Item-list calls run the one-kernel form (which checks the list on the device)
@@ -758,24 +765,26 @@ static int attention(const StrideAttentionParams* p, void* stream, const char* n
   if (!why.empty()) return fail(STRIDE_TC_EINVAL, std::string(name) + ": " + why);
   if (p->l.rows == 0) return 0;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if constexpr (!kExact) {
+  using KvT = typename std::conditional<kExact, float, uint16_t>::type;
+  {
     // records and page factors, then the row's KV page numbers
     const size_t blocks = (static_cast<size_t>(p->max_pages) * kAttnPage + page_tokens - 1) / page_tokens;
     const size_t lds = static_cast<size_t>(p->max_pages) * (8 + 4 * D + kHeadsPerGroup) * sizeof(float) + blocks * 4;
     const dim3 grid(p->l.rows * p->n_kv);
-    if (p->item_count == -1) {
-      if (D == 32) return fused<32, false>(grid, lds, st, *p, page_shift);
-      if (D == 64) return fused<64, false>(grid, lds, st, *p, page_shift);
-      return fused<128, false>(grid, lds, st, *p, page_shift);
+    if constexpr (!kExact) {
+      if (p->item_count == -1) {
+        if (D == 32) return fused<32, false>(grid, lds, st, *p, page_shift);
+        if (D == 64) return fused<64, false>(grid, lds, st, *p, page_shift);
+        return fused<128, false>(grid, lds, st, *p, page_shift);
+      }
     }
-    const bool fits = D == 32 ? fused_fits<32>(lds) : (D == 64 ? fused_fits<64>(lds) : fused_fits<128>(lds));
+    const bool fits = D == 32 ? fused_fits<32, KvT>(lds) : (D == 64 ? fused_fits<64, KvT>(lds) : fused_fits<128, KvT>(lds));
     if (fits && p->max_pages <= kListMaxPages && p->l.rows <= kListFusedMaxRows) {
-      if (D == 32) return fused<32, true>(grid, lds, st, *p, page_shift);
-      if (D == 64) return fused<64, true>(grid, lds, st, *p, page_shift);
-      return fused<128, true>(grid, lds, st, *p, page_shift);
+      if (D == 32) return fused<32, true, KvT, kExact>(grid, lds, st, *p, page_shift);
+      if (D == 64) return fused<64, true, KvT, kExact>(grid, lds, st, *p, page_shift);
+      return fused<128, true, KvT, kExact>(grid, lds, st, *p, page_shift);
     }
   }
-  using KvT = typename std::conditional<kExact, float, uint16_t>::type;
   if (p->item_count > 0) {
     const dim3 grid(p->item_count * p->n_kv);
     if (D == 32) hipLaunchKernelGGL((k_attn_page<32, KvT>), grid, dim3(64), 0, st, *p, page_shift);

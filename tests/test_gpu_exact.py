@@ -179,9 +179,16 @@ def test_embed_norm_compact(ref, m, dim):
     assert np.array_equal(comp.cpu().numpy()[:, :3].T.view(np.uint32), want[rows].view(np.uint32))
 
 
-@pytest.mark.parametrize("m,n_kv,hd,cap", [(1, 2, 64, 300), (7, 8, 64, 200), (5, 1, 128, 700), (6, 2, 32, 130)])
-def test_attention(ref, m, n_kv, hd, cap):
-    say("exact attention", m, n_kv, hd, cap)
+@pytest.mark.parametrize("m,n_kv,hd,cap,split", [(1, 2, 64, 300, False), (7, 8, 64, 200, False), (5, 1, 128, 700, False),
+                                                 (6, 2, 32, 130, False), (7, 8, 64, 200, True), (3, 2, 128, 2048, False)])
+def test_attention(ref, m, n_kv, hd, cap, split):
+    """The item list the reference's engine builds (every page of every row) runs
+    the one-kernel form; split = True lists each row's pages but its last in a
+    first call and the last pages in a second, whose combine takes the first
+    call's records from scratch; cap = 2048 (the reference's longest context,
+    src/kernels.h:18) at head_dim 128 is too long for the one kernel's LDS and
+    runs the page + combine pair."""
+    say("exact attention", m, n_kv, hd, cap, split)
     rng = np.random.default_rng(m + hd + cap)
     slots_n = 3
     q = rng.standard_normal((m, n_kv * 4 * hd)).astype(np.float32)
@@ -223,6 +230,13 @@ def test_attention(ref, m, n_kv, hd, cap):
     p.row_slot, p.row_pos, p.items, p.item_count = tc.ptr(rs), tc.ptr(rp), tc.ptr(items_d), items.size // 2
     p.scratch, p.max_pages, p.rec_floats, p.layer = tc.ptr(scratch), max_pages, rec, 0
     p.n_kv, p.n_q, p.head_dim, p.scale = n_kv, 4, hd, hd ** -0.5
+    if split:
+        first = np.array([[j, pg] for j in range(m) for pg in range(row_pos[j] // 64)], np.int32).reshape(-1)
+        second = np.array([[j, row_pos[j] // 64] for j in range(m)], np.int32).reshape(-1)
+        first_d, second_d = dev(first), dev(second)
+        p.items, p.item_count = tc.ptr(first_d), first.size // 2
+        exact.k_attention(p)
+        p.items, p.item_count = tc.ptr(second_d), second.size // 2
     exact.k_attention(p)
     torch.cuda.synchronize()
     got = back(out, m, n_kv * 4 * hd)
