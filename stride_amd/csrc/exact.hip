@@ -300,13 +300,27 @@ __global__ __launch_bounds__(64) void k_exact_gemm(typename Op::Params p, int nb
 // Embedding, RMSNorm, compaction.
 
 // h[k * stride + row] = widen(embed[token][k]); embed in [token/4][dim][4]
-// groups (src/kernels.cu:98-117).
-__global__ __launch_bounds__(64) void k_exact_embed(StrideEmbedParams p) {
+// groups (src/kernels.cu:98-117). A thread's kEmbedBatch elements are loaded
+// before any is stored, so the row costs one memory round trip per batch, not
+// one per element.
+constexpr int kEmbedBatch = 8;
+__global__ __launch_bounds__(256) void k_exact_embed(StrideEmbedParams p) {
   const int row = blockIdx.x;
   const int token = p.tokens[row];
   const uint16_t* src = p.embed + static_cast<int64_t>(token / 4) * p.dim * 4 + token % 4;
-  for (int k = threadIdx.x; k < p.dim; k += 64)
-    p.h[static_cast<int64_t>(k) * p.l.stride + row] = f32_of(static_cast<uint32_t>(src[static_cast<int64_t>(k) * 4]) << 16);
+  for (int k0 = threadIdx.x; k0 < p.dim; k0 += 256 * kEmbedBatch) {
+    uint16_t v[kEmbedBatch];
+#pragma unroll
+    for (int i = 0; i < kEmbedBatch; ++i) {
+      const int k = min(k0 + 256 * i, p.dim - 1);
+      v[i] = src[static_cast<int64_t>(k) * 4];
+    }
+#pragma unroll
+    for (int i = 0; i < kEmbedBatch; ++i) {
+      const int k = k0 + 256 * i;
+      if (k < p.dim) p.h[static_cast<int64_t>(k) * p.l.stride + row] = f32_of(static_cast<uint32_t>(v[i]) << 16);
+    }
+  }
 }
 
 // RMSNorm over four-dim units (src/kernels.cu:119-200): chain t sums the squares
@@ -483,7 +497,7 @@ int stride_k_embed(const StrideEmbedParams* p, void* stream) {
       p->l.stride < p->l.rows)
     return fail(STRIDE_TC_EINVAL, "k_embed: need rows >= 0, dim > 0, stride >= rows and pointers");
   if (p->l.rows == 0) return 0;
-  hipLaunchKernelGGL(k_exact_embed, dim3(p->l.rows), dim3(64), 0, static_cast<hipStream_t>(stream), *p);
+  hipLaunchKernelGGL(k_exact_embed, dim3(p->l.rows), dim3(256), 0, static_cast<hipStream_t>(stream), *p);
   return launched("k_embed");
 }
 
