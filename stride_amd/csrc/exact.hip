@@ -426,6 +426,89 @@ __global__ __launch_bounds__(64) void k_exact_norm(StrideNormParams p) {
   }
 }
 
+// The same RMSNorm with one 256-thread workgroup per lane group: every thread
+// loads its share of the lane group's inputs (and the gains it will scale them
+// with) in one memory round trip, the inputs into LDS; the 32 chains then run
+// over LDS in the order above, and all 256 threads scale and store. Serves rows
+// of up to kNormLdsItems 16-byte items (dim four-lane columns for J = 4, dim / 4
+// units for J = 1): 64 KiB of LDS.
+constexpr int kNormPer = 16;
+constexpr int kNormLdsItems = 256 * kNormPer;
+template <int J>
+__global__ __launch_bounds__(256) void k_exact_norm_lds(StrideNormParams p) {
+  extern __shared__ f32x4 vsm[];  // item i: unit i (J = 1) or column i's four lanes (J = 4)
+  __shared__ float part[kChains][J];
+  __shared__ float rs[J];
+  const int tid = threadIdx.x, block = blockIdx.x;
+  const int units = p.dim / 4, stride = p.l.stride;
+  const int items = J == 1 ? units : p.dim;
+  const float* in = J == 1 ? p.in : p.in + block * 4;
+  float* out = J == 1 ? p.out : p.out + block * 4;
+  f32x4 v[kNormPer], w4[J == 1 ? kNormPer : 1];
+  float wk[J == 1 ? 1 : kNormPer];
+#pragma unroll
+  for (int r = 0; r < kNormPer; ++r) {
+    const int i = tid + 256 * r;
+    if (i < items) {
+      if constexpr (J == 1) {
+        v[r] = *reinterpret_cast<const f32x4*>(in + 4 * i);
+        w4[r] = *reinterpret_cast<const f32x4*>(p.weight + 4 * i);
+      } else {
+        v[r] = *reinterpret_cast<const f32x4*>(in + static_cast<int64_t>(i) * stride);
+        wk[r] = p.weight[i];
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < kNormPer; ++r)
+    if (tid + 256 * r < items) vsm[tid + 256 * r] = v[r];
+  __syncthreads();
+  if (tid < kChains) {
+    float acc[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) acc[j] = 0.0f;
+    for (int u = tid; u < units; u += kChains) {
+      if constexpr (J == 1) {
+        const f32x4 x = vsm[u];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[0] = __builtin_fmaf(x[e], x[e], acc[0]);
+      } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const f32x4 x = vsm[u * 4 + c];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[j] = __builtin_fmaf(x[j], x[j], acc[j]);
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < J; ++j) part[tid][j] = acc[j];
+  }
+  __syncthreads();
+  if (tid < J) {
+    float sum = part[0][tid];
+    for (int i = 1; i < kChains; ++i) sum = sum + part[i][tid];
+    rs[tid] = 1.0f / sqrtf(sum / static_cast<float>(p.dim) + p.eps);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < kNormPer; ++r) {
+    const int i = tid + 256 * r;
+    if (i >= items) continue;
+    f32x4 o;
+    if constexpr (J == 1) {
+      const float q = rs[0];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = w4[r][e] * (v[r][e] * q);
+      *reinterpret_cast<f32x4*>(out + 4 * i) = o;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o[j] = wk[r] * (v[r][j] * rs[j]);
+      *reinterpret_cast<f32x4*>(out + static_cast<int64_t>(i) * stride) = o;
+    }
+  }
+}
+
 // out[k * lm_stride + l] = in[k * stride + lm_rows[l]] (src/kernels.cu:365-380).
 __global__ __launch_bounds__(64) void k_exact_compact(StrideCompactParams p) {
   const int k = blockIdx.x * 64 + threadIdx.x;
@@ -508,8 +591,15 @@ int stride_k_norm(const StrideNormParams* p, int32_t J, void* stream) {
   if (why.empty() && p->l.rows > 0 && (!p->in || !p->out || !p->weight)) why = "missing pointer";
   if (!why.empty()) return fail(STRIDE_TC_EINVAL, "k_norm: " + why);
   if (p->l.rows == 0) return 0;
-  const dim3 grid((p->l.lane_groups + 1) / 2);
   hipStream_t st = static_cast<hipStream_t>(stream);
+  const int items = J == 1 ? p->dim / 4 : p->dim;
+  if (items <= kNormLdsItems) {
+    const size_t lds = static_cast<size_t>(items) * 16;
+    if (J == 1) hipLaunchKernelGGL(k_exact_norm_lds<1>, dim3(p->l.lane_groups), dim3(256), lds, st, *p);
+    else hipLaunchKernelGGL(k_exact_norm_lds<4>, dim3(p->l.lane_groups), dim3(256), lds, st, *p);
+    return launched("k_norm");
+  }
+  const dim3 grid((p->l.lane_groups + 1) / 2);
   if (J == 1) hipLaunchKernelGGL(k_exact_norm<1>, grid, dim3(64), 0, st, *p);
   else hipLaunchKernelGGL(k_exact_norm<4>, grid, dim3(64), 0, st, *p);
   return launched("k_norm");

@@ -150,8 +150,11 @@ def test_qkv(ref, m, hd):
                                   rv[j, g * hd:(g + 1) * hd].view(np.uint32))
 
 
-@pytest.mark.parametrize("m,dim", [(1, 2048), (7, 2048), (13, 512)])
+@pytest.mark.parametrize("m,dim", [(1, 2048), (7, 2048), (13, 512), (6, 2052), (3, 4096), (1, 16384), (5, 8192),
+                                   (1, 20480)])
 def test_embed_norm_compact(ref, m, dim):
+    """Up to 4096 sixteen-byte items per lane group (dim for four-lane groups,
+    dim / 4 for one row) the norm stages its inputs in LDS; beyond, it streams them."""
     say("exact embed/norm/compact", m, dim)
     rng = np.random.default_rng(m + dim)
     vocab = 301
