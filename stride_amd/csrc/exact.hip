@@ -108,6 +108,10 @@ __device__ __forceinline__ void chain(const uint16_t* wg, const float* x, int st
   }
 }
 
+// Columns per slice of the sliced GEMM below: 32 lines of 8, so a slice holds
+// exactly one line of each chain.
+constexpr int kSlice = 256;
+
 // ---------------------------------------------------------------------------
 // GEMM-shaped operators: Op supplies the weight group(s) of a block and the
 // epilogue on the folded sums y[m][r * J + j].
@@ -116,6 +120,7 @@ struct ResidualOp {  // src/kernels.cu:294-325
   using Params = StrideGemmResidualParams;
   static constexpr int kMats = 1;
   static int groups(const Params& p) { return p.m.groups; }
+  static bool cols_sliced(const Params& p) { return p.m.cols % kSlice == 0; }
   __device__ static const uint16_t* w(const Params& p, int, int group, int& cols) {
     cols = p.m.cols;
     return p.m.w + static_cast<int64_t>(group) * p.m.cols * 4;
@@ -133,6 +138,7 @@ struct Mlp13Op {  // src/kernels.cu:329-363
   using Params = StrideMlp13Params;
   static constexpr int kMats = 2;
   static int groups(const Params& p) { return p.w1.groups; }
+  static bool cols_sliced(const Params& p) { return p.w1.cols % kSlice == 0 && p.w3.cols == p.w1.cols; }
   __device__ static const uint16_t* w(const Params& p, int m, int group, int& cols) {
     const StrideGemmMat& mm = m == 0 ? p.w1 : p.w3;
     cols = mm.cols;
@@ -150,6 +156,7 @@ struct LmFullOp {  // src/kernels.cu:427-452
   using Params = StrideLmFullParams;
   static constexpr int kMats = 1;
   static int groups(const Params& p) { return p.m.groups; }
+  static bool cols_sliced(const Params& p) { return p.m.cols % kSlice == 0; }
   __device__ static const uint16_t* w(const Params& p, int, int group, int& cols) {
     cols = p.m.cols;
     return p.m.w + static_cast<int64_t>(group) * p.m.cols * 4;
@@ -166,6 +173,7 @@ struct LmGreedyOp {  // src/kernels.cu:383-425
   using Params = StrideLmGreedyParams;
   static constexpr int kMats = 1;
   static int groups(const Params& p) { return p.m.groups; }
+  static bool cols_sliced(const Params& p) { return p.m.cols % kSlice == 0; }
   __device__ static const uint16_t* w(const Params& p, int, int group, int& cols) {
     cols = p.m.cols;
     return p.m.w + static_cast<int64_t>(group) * p.m.cols * 4;
@@ -194,6 +202,7 @@ struct QkvOp {  // src/kernels.cu:204-284
   using Params = StrideQkvParams;
   static constexpr int kMats = 1;
   static int groups(const Params& p) { return p.q.groups + 2 * p.k.groups; }
+  static bool cols_sliced(const Params& p) { return p.q.cols % kSlice == 0; }  // k and v: the same cols
   __device__ static const uint16_t* w(const Params& p, int, int gi, int& cols) {
     const StrideGemmMat& m = gi < p.q.groups ? p.q : (gi < p.q.groups + p.k.groups ? p.k : p.v);
     const int group = gi < p.q.groups ? gi : (gi < p.q.groups + p.k.groups ? gi - p.q.groups : gi - p.q.groups - p.k.groups);
@@ -294,6 +303,132 @@ __global__ __launch_bounds__(64) void k_exact_gemm(typename Op::Params p, int nb
   __syncthreads();
   if (live)
     for (int i = 0; i < nlg; ++i) Op::template finish<J>(p, group, lg0 + i, t, ys[half][i]);
+}
+
+// Sliced form (four batch lanes per reference block, columns a multiple of
+// kSlice): a workgroup of NWV waves runs NB = 2 * NWV reference blocks, i.e. NB
+// consecutive weight groups with one set of LG lane groups, so the blocks share
+// x. K is taken kSlice columns at a time: slice s holds line 32 * s + t of chain
+// t, so each lane still chains its lines in ascending order and every output's
+// operations are those of chain() (and of the reference). The slice's x is
+// staged once per workgroup in LDS (double buffered, the next slice's loads in
+// flight while the current one is summed), laid out so that lane t's reads of a
+// column are consecutive 16-byte words; each lane loads its own weight line one
+// slice ahead. The matrices of a paired GEMM are swept one after the other, and
+// each one's partials are folded and finished as in k_exact_gemm.
+template <class Op, int LG, int NWV>
+__global__ __launch_bounds__(64 * NWV) void k_exact_gemm_s(typename Op::Params p, int nsets, int ngroups) {
+  constexpr int M = Op::kMats;
+  constexpr int NB = 2 * NWV;
+  constexpr int NO = 16;                     // outputs per reference block (4 rows x 4 lanes)
+  constexpr int XS = kSlice * LG;            // staged f32x4 per slice: one per column and lane group
+  constexpr int NT = 64 * NWV;
+  constexpr int XPER = (XS + NT - 1) / NT;   // staging loads per thread
+  __shared__ f32x4 xs[2 * XS];
+  __shared__ float part[NB][kChains][NO * LG];
+  __shared__ float ys[NB][LG][M][16];
+  const int tid = threadIdx.x, wave = tid >> 6, half = (tid >> 5) & 1, t = tid & 31;
+  const int b = wave * 2 + half;
+  const int w = exact_wg_order(blockIdx.x, gridDim.x);
+  const int set = w % nsets;
+  const int group = (w / nsets) * NB + b;
+  const bool live = group < ngroups;
+  const int lg0 = set * LG, nlg = min(LG, p.l.lane_groups - lg0);
+
+  // Staging: item q of a slice is column c = q / LG, lane group q % LG (clamped
+  // to the last live one); column 8 * l + e (line l, column e of the line) sits
+  // at (e * 32 + l) * LG + i.
+  f32x4 xr[XPER];
+  auto load_x = [&](int sl) {
+#pragma unroll
+    for (int r = 0; r < XPER; ++r) {
+      const int q = tid + r * NT;
+      if (q < XS) {
+        const int c = q / LG, i = min(q % LG, nlg - 1);
+        xr[r] = *reinterpret_cast<const f32x4*>(p.x + static_cast<int64_t>(sl * kSlice + c) * p.l.stride + 4 * (lg0 + i));
+      }
+    }
+  };
+  auto store_x = [&](int buf) {
+#pragma unroll
+    for (int r = 0; r < XPER; ++r) {
+      const int q = tid + r * NT;
+      if (q < XS) {
+        const int c = q / LG, i = q % LG, l = c >> 3, e = c & 7;
+        xs[buf * XS + (e * 32 + l) * LG + i] = xr[r];
+      }
+    }
+  };
+
+  unroll<M>([&](auto mm) {
+    constexpr int m = decltype(mm)::value;
+    int cols = 0;
+    const uint16_t* wg = Op::w(p, m, min(group, ngroups - 1), cols);
+    const int nsl = cols / kSlice;
+    u32x4 wl[2][4];  // this lane's weight line of the current and the next slice
+    auto load_w = [&](int sl, auto buf) {
+      const u32x4* src = reinterpret_cast<const u32x4*>(wg + static_cast<int64_t>(sl * kChains + t) * 32);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) wl[decltype(buf)::value][q] = src[q];
+    };
+    float acc[NO * LG];
+#pragma unroll
+    for (int e = 0; e < NO * LG; ++e) acc[e] = 0.0f;
+    auto step = [&](auto buf) {
+      constexpr int c2 = decltype(buf)::value;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int c = 2 * q + h;  // column c of the line
+          const float wv[4] = {lo_half(wl[c2][q][2 * h]), hi_half(wl[c2][q][2 * h]), lo_half(wl[c2][q][2 * h + 1]),
+                               hi_half(wl[c2][q][2 * h + 1])};
+#pragma unroll
+          for (int i = 0; i < LG; ++i) {
+            const f32x4 xc = xs[c2 * XS + (c * 32 + t) * LG + i];
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+              for (int j = 0; j < 4; ++j) acc[(i * 4 + r) * 4 + j] = __builtin_fmaf(wv[r], xc[j], acc[(i * 4 + r) * 4 + j]);
+          }
+        }
+      }
+    };
+    load_x(0);
+    load_w(0, std::integral_constant<int, 0>{});
+    store_x(0);
+    __syncthreads();
+    // Slices in pairs so that the register and LDS buffers are compile-time.
+    // The next slice's loads are issued unconditionally (the last slice's again
+    // after it, into buffers nobody reads), so every pass waits on the same loads.
+    int sl = 0;
+    auto one = [&](auto cur) {
+      constexpr int c = decltype(cur)::value;
+      const int nx = min(sl + 1, nsl - 1);
+      load_x(nx);
+      load_w(nx, std::integral_constant<int, c ^ 1>{});
+      step(cur);
+      store_x(c ^ 1);
+      __syncthreads();
+      ++sl;
+    };
+    while (sl < nsl) {
+      one(std::integral_constant<int, 0>{});
+      if (sl < nsl) one(std::integral_constant<int, 1>{});
+    }
+    // Partials of this matrix, folded left to right per output.
+#pragma unroll
+    for (int e = 0; e < NO * LG; ++e) part[b][t][e] = acc[e];
+    __syncthreads();
+    for (int e = t; e < NO * LG; e += kChains) {
+      float y = part[b][0][e];
+      for (int i = 1; i < kChains; ++i) y = y + part[b][i][e];
+      ys[b][e / NO][m][e % NO] = y;
+    }
+    __syncthreads();
+  });
+  if (live)
+    for (int i = 0; i < nlg; ++i) Op::template finish<4>(p, group, lg0 + i, t, ys[b][i]);
 }
 
 // ---------------------------------------------------------------------------
@@ -550,8 +685,18 @@ int run_gemm(const typename Op::Params& p, int J, void* stream, const char* what
   const int lg = J == 1 ? 1 : LG;
   const int nblocks = Op::groups(p) * ((p.l.lane_groups + lg - 1) / lg);
   if (p.l.rows == 0 || nblocks == 0) return 0;
-  const dim3 grid((nblocks + 1) / 2);
   hipStream_t st = static_cast<hipStream_t>(stream);
+  // Four batch lanes per reference block: the sliced form shares x over eight
+  // weight groups. (One lane: the loads are weight-bound, and the streaming
+  // form keeps more of them in flight.)
+  if (J == 4 && Op::cols_sliced(p)) {
+    constexpr int NWV = 4;
+    const int sets = (p.l.lane_groups + lg - 1) / lg;
+    const dim3 sgrid(((Op::groups(p) + 2 * NWV - 1) / (2 * NWV)) * sets);
+    hipLaunchKernelGGL((k_exact_gemm_s<Op, LG, NWV>), sgrid, dim3(64 * NWV), 0, st, p, sets, Op::groups(p));
+    return launched(what);
+  }
+  const dim3 grid((nblocks + 1) / 2);
   if (J == 1) hipLaunchKernelGGL((k_exact_gemm<Op, 1, 1>), grid, dim3(64), 0, st, p, nblocks);
   else hipLaunchKernelGGL((k_exact_gemm<Op, 4, LG>), grid, dim3(64), 0, st, p, nblocks);
   return launched(what);

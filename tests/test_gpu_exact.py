@@ -49,7 +49,9 @@ def back(t, rows, n):
     return t.cpu().numpy()[:n, :rows].T.copy()
 
 
-SHAPES = [(1, 2048, 2048), (7, 256, 512), (37, 512, 2048), (64, 2048, 8192)]
+# K a multiple of 256 runs the sliced four-lane kernel (eight weight groups per
+# workgroup: 25 groups leave dead blocks); K = 264 the streaming one.
+SHAPES = [(1, 2048, 2048), (7, 256, 512), (37, 512, 2048), (64, 2048, 8192), (9, 100, 512), (6, 256, 264)]
 
 
 @pytest.mark.parametrize("m,n,k", SHAPES)
