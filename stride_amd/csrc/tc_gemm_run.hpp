@@ -631,7 +631,7 @@ inline Pick pick_large(const Geometry& g, int T, int smax, int mats, int per) {
       if (T <= 12) return {0, 15};   // 13.6 us at M = 192
       if (T <= 19) return {0, 29};   // 14.1-14.2 us at M = 256-290
       if (T <= 24) return {1, 15};   // 17.8 us at M = 384
-      if (T <= 32) return {1, 12};   // 19.1 us at M = 512
+      if (T <= 40) return {1, 12};   // 19.1 / 20.6 us at M = 512 / 640
       if (T <= 80) return {1, 39};   // 16 waves on 128 x 128: 25.2 / 25.9 / 28.3 us at M = 768 / 1024 / 1280
       if (T <= 128) return {1, 33};  // straddling 12-row-tile blocks: 35.9 / 40.3 us at M = 1536 / 2048
       return {1, 38};                // 46.4 / 67.2 / 74.2 us at M = 2560 / 3072 / 4096
@@ -640,7 +640,8 @@ inline Pick pick_large(const Geometry& g, int T, int smax, int mats, int per) {
       if (T <= 16) return {3, 23};   // 22.1 / 22.1 / 23.6 us at M = 160 / 192 / 256
       if (T <= 20) return {3, 24};   // 26.8 us at M = 290
       if (T <= 32) return {3, 2};    // 29.1 / 30.6 us at M = 384 / 512
-      if (T <= 64) return {0, 30};   // 49.4 / 49.9 us at M = 768 / 1024
+      if (T <= 56) return {1, 14};   // 49.2 / 49.5 / 51.0 us at M = 640 / 768 / 896 (streaming: 70-72)
+      if (T <= 64) return {1, 12};   // 54.9 us at M = 1024 (streaming: 74.1)
       if (T <= 128) return {1, 39};  // 75.6 / 75.8 / 78.8 us at M = 1280 / 1536 / 2048
       if (T <= 160) return {1, 33};  // 100.2 us at M = 2560
       return {1, 23};                // 117.3 / 121.5 us at M = 3072 / 4096
@@ -649,8 +650,8 @@ inline Pick pick_large(const Geometry& g, int T, int smax, int mats, int per) {
     if (T <= 16) return {0, 27};     // 8.7 / 9.0 / 9.1 us at M = 160 / 192 / 256
     if (T <= 20) return {0, 59};     // 11.9 us at M = 290
     if (T <= 32) return {0, 29};     // 12.6 / 12.6 us at M = 384 / 512
-    if (T <= 48) return {1, 14};     // 17.7 us at M = 768
-    if (T <= 64) return {0, 30};     // 18.6 us at M = 1024
+    if (T <= 48) return {1, 14};     // 17.0 / 17.4 us at M = 640 / 768
+    if (T <= 64) return {1, 12};     // 18.3 / 18.6 us at M = 896 / 1024 (streaming: 31-32)
     if (T <= 128) return {1, 39};    // 23.9 / 24.1 / 27.1 us at M = 1280 / 1536 / 2048
     if (T <= 160) return {1, 33};    // 34.6 us at M = 2560
     return {1, 28};                  // 39.2 / 44.1 us at M = 3072 / 4096
