@@ -608,7 +608,7 @@ inline Pick pick_large(const Geometry& g, int T, int smax, int mats, int per) {
     if (T <= 16) return {3, 16};  // 24.6 / 24.1 / 26.1 us at M = 160 / 192 / 256
     if (T <= 20) return {3, 22};  // ten lane tiles per workgroup: 30.1 us at M = 290 (pipeline: 35.5)
     if (T <= 32) return {3, 14};  // 37.9 / 40.5 us at M = 384 / 512
-    if (T <= 40) return {1, 23};
+    if (T <= 40) return {3, 16};  // 55.3 us at M = 640 (pipeline: 69.4)
     return {1, 4};                // 256 x 256 blocks: 63.0 / 122.5 / 233.4 us at M = 1024 / 2048 / 4096
   }
   if (smax == 1) {  // LM head: weights to registers at 9-12 and 17-24 lane tiles (M = 160 / 290 / 384:
@@ -616,6 +616,7 @@ inline Pick pick_large(const Geometry& g, int T, int smax, int mats, int per) {
     // several lane groups re-read each weight chunk: plain weight loads
     if (T <= 12 || (T > 16 && T <= 20)) return {3, 28};  // 148 / 152 / 216 us at M = 160 / 192 / 290
     if (T > 20 && T <= 24) return {3, 25};               // 239 us at M = 384
+    if (T > 32 && T <= 40) return {3, 14};               // 366 us at M = 640 (pipeline: 388)
     return {1, 6};
   }
   if (smax == 2) {
