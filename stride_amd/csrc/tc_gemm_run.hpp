@@ -629,8 +629,7 @@ inline Pick pick_large(const Geometry& g, int T, int smax, int mats, int per) {
   if (smax == 4) {  // the split rule's few-row matrices (sweeps at M = 160 ... 4096)
     if (g.nseg == 3) {  // fused QKV
       if (T <= 10) return {0, 59};   // four split waves for the four splits: 10.6 us at M = 160 (12.5 with eight)
-      if (T <= 12) return {0, 15};   // 13.6 us at M = 192
-      if (T <= 19) return {0, 29};   // 14.1-14.2 us at M = 256-290
+      if (T <= 19) return {0, 29};   // 12.9 / 13.1 / 13.0 us at M = 192 / 256 / 290
       if (T <= 24) return {1, 15};   // 17.8 us at M = 384
       if (T <= 40) return {1, 12};   // 19.1 / 20.6 us at M = 512 / 640
       if (T <= 80) return {1, 39};   // 16 waves on 128 x 128: 25.2 / 25.9 / 28.3 us at M = 768 / 1024 / 1280
