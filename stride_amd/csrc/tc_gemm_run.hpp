@@ -640,8 +640,8 @@ inline Pick pick_large(const Geometry& g, int T, int smax, int mats, int per) {
       if (T <= 16) return {3, 23};   // 22.1 / 22.1 / 23.6 us at M = 160 / 192 / 256
       if (T <= 20) return {3, 24};   // 26.8 us at M = 290
       if (T <= 32) return {3, 2};    // 29.1 / 30.6 us at M = 384 / 512
-      if (T <= 56) return {1, 14};   // 49.2 / 49.5 / 51.0 us at M = 640 / 768 / 896 (streaming: 70-72)
-      if (T <= 64) return {1, 12};   // 54.9 us at M = 1024 (streaming: 74.1)
+      if (T <= 56) return {1, 14};   // 49.2 / 49.5 / 51.0 us at M = 640 / 768 / 896
+      if (T <= 64) return {0, 30};   // 50.9 us at M = 1024 (pipeline: 54.2)
       if (T <= 128) return {1, 39};  // 75.6 / 75.8 / 78.8 us at M = 1280 / 1536 / 2048
       if (T <= 160) return {1, 33};  // 100.2 us at M = 2560
       return {1, 23};                // 117.3 / 121.5 us at M = 3072 / 4096

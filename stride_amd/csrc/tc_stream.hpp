@@ -417,12 +417,37 @@ __global__ __launch_bounds__(kWave * WS * WR) void k_stream(Geometry g, typename
       __syncthreads();
     }
   } else {
-    if (nbatch > 0) {
-      // Batch b's loads go out while batch b - 1 is multiplied. The loop body
-      // runs while two more batches remain, so its loads are unconditional (a
-      // load behind a branch makes the compiler's wait before the next MFMAs
-      // assume the path without it), and a scheduling barrier keeps each batch's
-      // loads ahead of the previous batch's MFMAs.
+    // Batch b's loads go out while batch b - 1 is multiplied. With few
+    // accumulators and small batches (every decode configuration) the loop body
+    // runs while two more batches remain, so its loads are unconditional (a load
+    // behind a branch makes the compiler's wait before the next MFMAs assume the
+    // path without it), and a scheduling barrier keeps each batch's loads ahead
+    // of the previous batch's MFMAs. Wider blocks cannot hold both batches and
+    // the accumulators in registers that way (they spilled); they keep a loop
+    // the compiler may interleave.
+    constexpr bool kTwoBatch = R * M * LT * 4 <= 96 && 2 * U * (R * M + LT) * 4 <= 192;
+    if (nbatch > 0 && !kTwoBatch) {
+      load_w(a0, c0);
+      load_x(b0, c0);
+      int c = c0;
+      for (;;) {
+        if (c + U < cb) {
+          load_w(a1, c + U);
+          load_x(b1, c + U);
+        }
+        mma(a0, b0, 0);
+        c += U;
+        if (c >= cb) break;
+        if (c + U < cb) {
+          load_w(a0, c + U);
+          load_x(b0, c + U);
+        }
+        mma(a1, b1, 0);
+        c += U;
+        if (c >= cb) break;
+      }
+    }
+    if (nbatch > 0 && kTwoBatch) {
       load_w(a0, c0);
       load_x(b0, c0);
       int c = c0;
